@@ -1,0 +1,129 @@
+/* dense_reader.h: the C ABI of the MI355X (gfx950) dense_reader decode matmul.
+ *
+ * A weight-streaming matmul y = x @ w (* scale) for decode: x bf16 [M, K], w a block-float (bfloat8_b, bfloat4_b)
+ * or bf16 weight [K, N] packed once into this library's HBM layout, fp32 accumulation, output bf16 or fp32, with the
+ * fused output stages of the reference (per-column scales, SwiGLU/GeGLU, residual add, fp32 output, top-k records)
+ * and block lists (up to four weights written into one output by one launch).
+ *
+ * Every entry point takes plain device pointers and sizes and a hipStream_t (as void*), allocates nothing, and
+ * returns 0 or a DR_E* status (dr_status_string names it). Work is enqueued on the stream; nothing synchronises.
+ *
+ * Reference interfaces replaced (XylolabsInc/tensix-kernels, paths relative to its root):
+ *   dr_pack        <- dense_reader/linear.py:144-156 native_weight's conversion (ttnn.from_torch(..., dtype,
+ *                     TILE_LAYOUT)) and its column scale division (linear.py:149-151)
+ *   dr_unpack      <- dense_reader/linear.py:159-163 block_float / ttnn.to_torch of a weight (the held values)
+ *   dr_matmul      <- dense_reader/linear.py:828-1070 _launch's ttnn.generic_op(ios, ProgramDescriptor) with the
+ *                     kernels dense_reader.cpp, dense_compute.cpp and dense_writer.cpp
+ *   dr_topk_merge  <- the host merge of top-k records, dense_reader/linear.py:747-768 (records_host) followed by a
+ *                     best-k selection as lm_head_topk/lmhead.py:212-239 does on the host
+ *   dr_plan        <- dense_reader/linear.py:455-495 choose/plan (the work split, for inspection only)
+ */
+#ifndef DENSE_READER_H
+#define DENSE_READER_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* weight formats (the reference's ttnn.bfloat8_b, ttnn.bfloat4_b, ttnn.bfloat16) */
+#define DR_BFP8 0
+#define DR_BFP4 1
+#define DR_BF16 2
+
+/* statuses */
+#define DR_OK 0
+#define DR_EINVAL 1   /* an argument outside what the op takes (Python: AssertionError / ValueError) */
+#define DR_EHIP 2     /* a HIP runtime error (Python: RuntimeError) */
+#define DR_ERANGE 3   /* a size beyond a documented limit */
+
+/* Geometry of a packed weight of K rows (in) and N columns (out):
+ *   k_pad = K rounded up to 128, n_pad = N rounded up to 32 (or a multiple the caller asks for);
+ *   codes: n_pad / 16 panels x k_pad values; bytes = k_pad * n_pad (bfp8), k_pad * n_pad / 2 (bfp4),
+ *          2 * k_pad * n_pad (bf16);
+ *   exps:  one byte per (panel, k): k_pad * n_pad / 16 bytes (bfp8, bfp4; none for bf16). */
+int64_t dr_codes_bytes(int fmt, int k_pad, int n_pad);
+int64_t dr_exps_bytes(int fmt, int k_pad, int n_pad);
+
+/* Pack w [N=out rows][K=in columns] fp32 (device, row stride ld_w elements) as the weight [K, N] in format fmt:
+ * each 16 output columns at one k share one exponent (the reference's face row), values rounded as the reference's
+ * host conversion does. col_div (device [N] fp32, or NULL): row n of w divided by col_div[n] first (native_weight's
+ * col_scale). Columns n >= N and rows k >= K up to n_pad, k_pad hold zeros. */
+int dr_pack(const float* w, int64_t ld_w, int n, int k, int fmt, const float* col_div, void* codes, void* exps,
+            int n_pad, int k_pad, void* stream);
+
+/* The held values of a packed weight: out [K][ld_out] fp32 (device), columns 0 .. n-1. */
+int dr_unpack(const void* codes, const void* exps, int fmt, int n, int k, int n_pad, int k_pad, float* out,
+              int64_t ld_out, void* stream);
+
+/* One weight (or gate/up pair) of a launch: its output columns [col0, col0 + n_out) of y, n_out = n, or n / 2
+ * for an interleaved GLU weight (glu 1). */
+typedef struct dr_segment {
+    int32_t fmt;        /* DR_BFP8, DR_BFP4, DR_BF16 */
+    int32_t n;          /* the weight's columns (glu 1: 2 * the output's, gate and up tiles alternating) */
+    int32_t n_pad;      /* the packed weight's padded columns (a multiple of 32) */
+    int32_t glu;        /* 0 none; 1 interleave_glu weight; 2 gate in codes/exps, up in codes_up/exps_up */
+    const void* codes;
+    const void* exps;
+    const void* codes_up;
+    const void* exps_up;
+    const void* scale;    /* per weight column scales [n] or NULL (unit) */
+    const void* scale_up; /* glu 2: the up weight's scales or NULL */
+    int32_t scale_f32;    /* scales are fp32 (1) or bf16 (0) */
+    int32_t col0;         /* first output column in y, a multiple of 32 */
+} dr_segment;
+
+/* Top-k records: for every 32-column output tile t of the launch, one record at index slot0 + t holding, for each
+ * of the first `rows` rows, the best k values of that tile (highest first, ties to the lower column), written as
+ * rows * k keys then rows * k ids (uint32 words). fp32 0: keys are the reference's bf16 keys of the bf16 output
+ * (0 empty) and ids base + column (0xFFFFFFFF empty); fp32 1: keys are the fp32 scores' bits (-inf empty) and ids
+ * int32 (-1 empty). */
+typedef struct dr_topk {
+    void* records;       /* [records_cap][2 * rows * k] uint32, or NULL: no top-k */
+    int32_t k;           /* 1 .. 32 */
+    int32_t rows;        /* 1 .. 32, at most the launch's rows */
+    int32_t slot0;
+    int32_t records_cap;
+    int32_t n_valid;     /* output columns taking part (columns >= n_valid never enter) */
+    int64_t base;        /* id of output column 0 */
+    int32_t write_y;     /* 0: y is not written */
+    int32_t fp32;
+} dr_topk;
+
+typedef struct dr_launch {
+    const void* x;       /* [m][ldx] bf16 */
+    int32_t m, k, ldx;
+    void* y;             /* [m][ldy] bf16 or fp32 */
+    int32_t ldy;
+    int32_t y_f32;
+    const void* residual; /* [m][ldr] bf16 or NULL */
+    int32_t ldr;
+    int32_t residual_mode; /* 1 epilogue: y = acc + r; 2 preload: the sum starts at r */
+    int32_t act;         /* GLU activation: 0 silu (SwiGLU), 1 gelu_tanh (GeGLU) */
+    int32_t nseg;        /* 1 .. 4 */
+    dr_segment seg[4];
+    dr_topk topk;
+    void* stream;        /* hipStream_t */
+} dr_launch;
+
+/* y = the launch's fused matmul. Allocates nothing. */
+int dr_matmul(const dr_launch* launch);
+
+/* The best k_out of records [n_records][2 * rows * k] (as dr_topk writes them) per row: vals [rows][k_out] fp32
+ * (-inf empty), ids [rows][k_out] int32 (-1 empty), highest first, ties to the lower id. k_out <= 64. */
+int dr_topk_merge(const void* records, int n_records, int rows, int k, int fp32, int k_out, float* vals,
+                  int32_t* ids, void* stream);
+
+/* The work split for K and M: chunks (waves per output tile, each a K range of kch values) and the rows a pass
+ * takes. For inspection; results depend only on what this returns. */
+int dr_plan(int k, int m, int32_t* chunks, int32_t* kch, int32_t* rows_per_pass);
+
+const char* dr_status_string(int status);
+int dr_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

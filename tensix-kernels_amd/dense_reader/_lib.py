@@ -1,0 +1,133 @@
+"""ctypes binding of libdense_reader.so (the C ABI declared in include/dense_reader.h).
+
+The library is built in-tree (`python -c "import __graft_entry__; __graft_entry__.build()"` at the repository root,
+or `make -C tensix-kernels_amd/dense_reader/csrc`). There is no fallback: without the library every op raises.
+"""
+
+import ctypes
+import os
+from pathlib import Path
+
+LIB_NAME = "libdense_reader.so"
+LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
+
+DR_OK, DR_EINVAL, DR_EHIP, DR_ERANGE = 0, 1, 2, 3
+
+# every symbol include/dense_reader.h declares
+SYMBOLS = (
+    "dr_codes_bytes",
+    "dr_exps_bytes",
+    "dr_pack",
+    "dr_unpack",
+    "dr_matmul",
+    "dr_topk_merge",
+    "dr_plan",
+    "dr_status_string",
+    "dr_version",
+)
+
+c_int, c_int32, c_int64, c_void_p = ctypes.c_int, ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p
+
+
+class Segment(ctypes.Structure):
+    _fields_ = [
+        ("fmt", c_int32),
+        ("n", c_int32),
+        ("n_pad", c_int32),
+        ("glu", c_int32),
+        ("codes", c_void_p),
+        ("exps", c_void_p),
+        ("codes_up", c_void_p),
+        ("exps_up", c_void_p),
+        ("scale", c_void_p),
+        ("scale_up", c_void_p),
+        ("scale_f32", c_int32),
+        ("col0", c_int32),
+    ]
+
+
+class TopK(ctypes.Structure):
+    _fields_ = [
+        ("records", c_void_p),
+        ("k", c_int32),
+        ("rows", c_int32),
+        ("slot0", c_int32),
+        ("records_cap", c_int32),
+        ("n_valid", c_int32),
+        ("base", c_int64),
+        ("write_y", c_int32),
+        ("fp32", c_int32),
+    ]
+
+
+class Launch(ctypes.Structure):
+    _fields_ = [
+        ("x", c_void_p),
+        ("m", c_int32),
+        ("k", c_int32),
+        ("ldx", c_int32),
+        ("y", c_void_p),
+        ("ldy", c_int32),
+        ("y_f32", c_int32),
+        ("residual", c_void_p),
+        ("ldr", c_int32),
+        ("residual_mode", c_int32),
+        ("act", c_int32),
+        ("nseg", c_int32),
+        ("seg", Segment * 4),
+        ("topk", TopK),
+        ("stream", c_void_p),
+    ]
+
+
+_lib = None
+
+
+def lib():
+    """The loaded library (RuntimeError when it is not built)."""
+    global _lib
+    if _lib is None:
+        path = os.environ.get("DENSE_READER_LIB", str(LIB_PATH))
+        if not Path(path).exists():
+            raise RuntimeError(
+                f"dense_reader: {path} is not built (run __graft_entry__.build() or make in dense_reader/csrc); "
+                "there is no fallback path"
+            )
+        L = ctypes.CDLL(path)
+        L.dr_codes_bytes.restype = c_int64
+        L.dr_codes_bytes.argtypes = [c_int, c_int, c_int]
+        L.dr_exps_bytes.restype = c_int64
+        L.dr_exps_bytes.argtypes = [c_int, c_int, c_int]
+        L.dr_pack.restype = c_int
+        L.dr_pack.argtypes = [c_void_p, c_int64, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p]
+        L.dr_unpack.restype = c_int
+        L.dr_unpack.argtypes = [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_int64, c_void_p]
+        L.dr_matmul.restype = c_int
+        L.dr_matmul.argtypes = [ctypes.POINTER(Launch)]
+        L.dr_topk_merge.restype = c_int
+        L.dr_topk_merge.argtypes = [c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p]
+        L.dr_plan.restype = c_int
+        L.dr_plan.argtypes = [c_int, c_int, ctypes.POINTER(c_int32), ctypes.POINTER(c_int32), ctypes.POINTER(c_int32)]
+        L.dr_status_string.restype = ctypes.c_char_p
+        L.dr_status_string.argtypes = [c_int]
+        L.dr_version.restype = c_int
+        L.dr_version.argtypes = []
+        _lib = L
+    return _lib
+
+
+def check(status, what):
+    """Raise for a non-zero status: ValueError for an argument the op does not take, else RuntimeError."""
+    if status == DR_OK:
+        return
+    msg = f"{what}: {lib().dr_status_string(status).decode()} (status {status})"
+    if status in (DR_EINVAL, DR_ERANGE):
+        raise ValueError(msg)
+    raise RuntimeError(msg)
+
+
+def plan(k, m):
+    """(chunks, kch, rows_per_pass) of the library's work split for K and M."""
+    c, ch, r = c_int32(), c_int32(), c_int32()
+    check(lib().dr_plan(k, m, ctypes.byref(c), ctypes.byref(ch), ctypes.byref(r)), "dr_plan")
+    return c.value, ch.value, r.value

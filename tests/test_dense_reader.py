@@ -1,0 +1,275 @@
+"""The dense_reader op on the GPU against the CPU oracle (after XylolabsInc/tensix-kernels
+dense_reader/tests/test_dense_reader.py, whose nine tests are mirrored here test for test, plus the packing checks the
+MI355X layout needs).
+
+Reference: x rounded to bf16 times the weight's own held values, in float64 (oracle.ref). Bars (the reference's):
+relative Frobenius error below 1 % and PCC above 0.9999 for bf16 outputs, 0.1 % for the fp32 output; bit for bit where
+two configurations of the op must agree (work-split knobs, repeated calls, a block list against one call per block,
+the top-k records against the op's own output) and for the packing (codes, exponents, held values).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from common import device as cdev
+from common.testing import check, raises, same
+from dense_reader import linear
+from oracle import dense_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = {"bfp8": linear.bfloat8_b, "bfp4": linear.bfloat4_b, "bf16": linear.bfloat16}
+
+
+def x_input(device, m, k, seed):
+    x = O.x_input(m, k, seed)  # randn with outlier channels 0..3 (test_dense_reader.py:28-39)
+    return x, x.to(torch.bfloat16).reshape(1, 1, m, k).to(device.torch)
+
+
+matrix = O.matrix
+
+
+def held(tw, n):
+    return linear.held(tw, n).cpu()
+
+
+def host(y, m, n):
+    return y.float().cpu().reshape(-1, y.shape[-1])[:m, :n]
+
+
+ref = O.ref
+
+
+def _special(n, k, seed):
+    """[out, in] weights with zeros, a denormal, tiny values, ties and columns of very different size."""
+    w = matrix(n, k, seed)
+    w[::5, ::7] *= 50
+    w[5, 3] = 0.0
+    w[9, 7] = -1e-30
+    w[1, 1] = 1e-40
+    w[:16, 2] = 0.0
+    w[16:24, 4] = torch.tensor([1.0, 0.5, 0.25, 0.125, 0.875, 1.875, -0.4375, 0.0625])
+    return w
+
+
+@pytest.mark.parametrize("fmt", ["bfp8", "bfp4", "bf16"])
+def test_pack_bitexact(device, fmt):
+    n, k = 200, 160  # N padded to 256 (8 banks x 32), K to 256
+    wt = _special(n, k, 30)
+    tw, _ = linear.native_weight(device, wt, DTYPES[fmt])
+    codes, exps = O.to_layout(wt.T.contiguous(), fmt, n_pad=tw.n_pad)
+    same(f"{fmt} codes against the reference-format conversion", tw.codes.cpu(), torch.from_numpy(codes))
+    if exps is not None:
+        same(f"{fmt} exponents", tw.exps.cpu(), torch.from_numpy(exps))
+    same(f"{fmt} held values", held(tw, n), torch.from_numpy(O.held(wt.T.contiguous(), fmt)))
+
+
+def test_col_scale_pack(device):
+    n, k = 96, 128
+    wt = matrix(n, k, 31)
+    wt[: n // 2] *= 40
+    tw, ts = linear.native_weight(device, wt, linear.bfloat8_b, col_scale=True)
+    c = O.bf16_ceil(wt.abs().amax(dim=1).clamp(min=1e-8))
+    same("column scales", ts.float().cpu().reshape(-1), c)
+    same("held values of w / c", held(tw, n), torch.from_numpy(O.held((wt / c[:, None]).T.contiguous(), "bfp8")))
+
+
+def test_formats(device):
+    k, n = 1024, 2048
+    wt = matrix(n, k, 2)
+    for fmt, dtype in DTYPES.items():
+        tw, _ = linear.native_weight(device, wt, dtype)
+        wk = held(tw, n)
+        for m in (1, 7, 32):
+            x, tx = x_input(device, m, k, 1 + m)
+            check(f"{fmt} rows {m} K {k} N {n}", host(linear.matmul(tx, tw, None), m, n), ref(x, wk))
+
+
+def test_scales_interleaved_prefill(device):
+    k, n = 1024, 1536
+    wt = matrix(n, k, 3)
+    wt[: n // 2] *= 40  # columns of very different size
+    tw, ts = linear.native_weight(device, wt, linear.bfloat8_b, col_scale=True)
+    c = ts.float().cpu().reshape(-1)[:n]
+    wk = held(tw, n)
+    for m in (1, 100, 200):  # decode; prefill rows in passes
+        x, tx = x_input(device, m, k, 4 + m)
+        check(f"bfp8 column scales rows {m}", host(linear.matmul(tx, tw, ts), m, n), ref(x, wk, c))
+    ti, _ = linear.native_weight(device, wt, linear.bfloat8_b, sharded=False)
+    x, tx = x_input(device, 3, k, 5)
+    check("bfp8 interleaved weight rows 3", host(linear.matmul(tx, ti, None), 3, n), ref(x, held(ti, n)))
+
+
+def test_split_shares_bitwise(device):
+    """The reference's work-split knobs change nothing; repeated calls are bit-identical."""
+    k, n, m = 2048, 2048, 3
+    x, tx = x_input(device, m, k, 6)
+    tw, _ = linear.native_weight(device, matrix(n, k, 7), linear.bfloat4_b)
+    base = host(linear.matmul(tx, tw, None), m, n)
+    try:
+        for share in (0.6, 2 / 3, 0.75):
+            linear.SPLIT_SHARE = share
+            same(f"split share {share:.3f} against 0.5", host(linear.matmul(tx, tw, None), m, n), base)
+        linear.SPLIT_SHARE = 0.5
+        same("one loader against two", host(linear.matmul(tx, tw, None, split=False), m, n), base)
+        linear.REQ_TILES = 3
+        same("requests of 3 tiles against one a row", host(linear.matmul(tx, tw, None), m, n), base)
+    finally:
+        linear.SPLIT_SHARE, linear.REQ_TILES = 0.5, 0
+    for i in range(3):
+        same(f"repeat {i}", host(linear.matmul(tx, tw, None), m, n), base)
+
+
+def test_glu(device):
+    k, n = 1024, 1024
+    gate, up = matrix(n, k, 8), matrix(n, k, 9)
+    tw, _ = linear.native_weight(device, linear.interleave_glu(gate, up), linear.bfloat8_b)
+    tg, _ = linear.native_weight(device, gate, linear.bfloat8_b)
+    tu, _ = linear.native_weight(device, up, linear.bfloat8_b)
+    gk, uk = held(tg, n), held(tu, n)
+    for m in (3, 20):
+        x, tx = x_input(device, m, k, 10 + m)
+        g, u = ref(x, gk).double(), ref(x, uk).double()
+        swi = (torch.nn.functional.silu(g) * u).float()
+        gel = (torch.nn.functional.gelu(g, approximate="tanh") * u).float()
+        check(f"swiglu interleaved rows {m}", host(linear.linear(tx, tw, None, activation="swiglu"), m, n), swi)
+        check(f"swiglu two weights rows {m}", host(linear.linear(tx, (tg, tu), None, activation="swiglu"), m, n), swi)
+        check(f"geglu interleaved rows {m}", host(linear.linear(tx, tw, None, activation="geglu"), m, n), gel)
+        check(f"geglu two weights rows {m}", host(linear.linear(tx, (tg, tu), None, activation="geglu"), m, n), gel)
+
+
+def test_residual_out32(device):
+    k, n, m = 1024, 2048, 5
+    x, tx = x_input(device, m, k, 12)
+    wt = matrix(n, k, 13)
+    tw, _ = linear.native_weight(device, wt, linear.bfloat8_b)
+    wk = held(tw, n)
+    res = torch.randn(32, n, generator=torch.Generator().manual_seed(27))
+    resb = res.to(torch.bfloat16)
+    tr = resb.reshape(1, 1, 32, n).to(device.torch)
+    want = ref(x, wk) + resb[:m].float()
+    for mode in ("epilogue", "preload"):
+        y = linear.matmul(tx, tw, None, residual=tr, residual_mode=mode)
+        check(f"residual {mode} rows {m}", host(y, m, n), want)
+    y = linear.linear(tx, tw, None, out_dtype=linear.float32, fidelity="hifi4")
+    check(f"fp32 output rows {m}", host(y, m, n), ref(x, wk), rel=1e-3, pcc=0.999999)
+    # in place: out is the residual itself
+    tr2 = tr[:, :, :m].contiguous()
+    y = linear.matmul(tx, tw, None, residual=tr2, out=tr2)
+    assert y is tr2
+    check(f"residual in place rows {m}", host(y, m, n), want)
+
+
+def test_topk_records(device):
+    k, n, rows, kk = 1024, 2048, 3, 8
+    x, tx = x_input(device, 32, k, 14)
+    tw, _ = linear.native_weight(device, matrix(n, k, 15), linear.bfloat4_b)
+    for n_valid, base in ((n, 0), (n - 37, 1000)):
+        r = linear.topk_result(device, linear.topk_slots(n), rows, kk)
+        spec = {"r": r, "k": kk, "rows": rows, "slot0": 0, "base": base, "n": n_valid, "write_y": True}
+        y = host(linear.matmul(tx, tw, None, topk=spec), rows, n)
+        vals, idx = linear.topk_records(r, rows, kk)
+        for t in range(rows):
+            ok = idx[t] >= 0
+            got = vals[t][ok]
+            col = idx[t][ok] - base
+            assert int(col.min()) >= 0 and int(col.max()) < n_valid, (col.min(), col.max())
+            same(f"top-k records row {t} (n {n_valid}, base {base}): values at their ids", y[t][col], got)
+            top = torch.sort(got, descending=True).values[:kk]
+            same(f"top-k records row {t}: the best {kk} of the row", top, torch.topk(y[t][:n_valid], kk).values)
+        # the records exactly as the oracle writes them from this output (per 32-column tile, ties to the lower id)
+        words = O.tile_topk(y.numpy(), rows, kk, n_valid, base)
+        same("records against the oracle's", r.cpu().reshape(-1, 2 * rows * kk), torch.from_numpy(words.view(np.int32)))
+
+
+def test_block_list_bitwise(device):
+    k, m = 1024, 3
+    x, tx = x_input(device, m, k, 16)
+    a, _ = linear.native_weight(device, matrix(1024, k, 17), linear.bfloat8_b)
+    b, _ = linear.native_weight(device, matrix(1024, k, 18), linear.bfloat8_b)
+    width = 2048 + 64  # a gap of two tiles between the blocks
+    one = linear.matmul(tx, [(a, 0), (b, 34)], None)
+    two = torch.zeros(1, 1, m, width, dtype=torch.bfloat16, device=device.torch)
+    linear.matmul(tx, a, None, out=two, col0=0)
+    linear.matmul(tx, b, None, out=two, col0=34)
+    ho, ht = host(one, m, width), host(two, m, width)
+    same(
+        "block list against one call per block",
+        torch.cat([ho[:, :1024], ho[:, 1088:]], 1),
+        torch.cat([ht[:, :1024], ht[:, 1088:]], 1),
+    )
+    g1, _ = linear.native_weight(device, matrix(512, k, 19), linear.bfloat8_b)
+    u1, _ = linear.native_weight(device, matrix(512, k, 20), linear.bfloat8_b)
+    g2, _ = linear.native_weight(device, matrix(512, k, 21), linear.bfloat8_b)
+    u2, _ = linear.native_weight(device, matrix(512, k, 22), linear.bfloat8_b)
+    for act in ("swiglu", "geglu"):
+        one = linear.linear(tx, [((g1, u1), 0), ((g2, u2), 16)], None, activation=act)
+        p1 = linear.linear(tx, (g1, u1), None, activation=act)
+        p2 = linear.linear(tx, (g2, u2), None, activation=act)
+        same(
+            f"{act} block list against one call per pair",
+            host(one, m, 1024),
+            torch.cat([host(p1, m, 512), host(p2, m, 512)], 1),
+        )
+
+
+def test_max_banks(device):
+    k, n, m = 1024, 1024, 2
+    banks = cdev.dram_banks(device)
+    fewer = max(1, banks // 2)
+    x, tx = x_input(device, m, k, 23)
+    wt = matrix(n, k, 24)
+    tw, _ = linear.native_weight(device, wt, linear.bfloat8_b, max_banks=fewer)
+    assert tw.memory_config().banks == fewer
+    check(f"weight over {fewer} of {banks} banks", host(linear.matmul(tx, tw, None), m, n), ref(x, held(tw, n)))
+    full, _ = linear.native_weight(device, wt, linear.bfloat8_b)
+    if banks > fewer:
+        raises(
+            f"a weight over {banks} banks with max_banks {fewer}",
+            ValueError,
+            lambda: linear.matmul(tx, full, None, max_banks=fewer),
+        )
+
+
+def test_linear_rank3(device):
+    k, n, m = 1024, 1024, 4
+    x, tx = x_input(device, m, k, 25)
+    wt = matrix(n, k, 26)
+    tw, _ = linear.native_weight(device, wt, linear.bfloat8_b)
+    x3 = tx.reshape(1, m, k)
+    y = linear.linear(x3, tw, None, activation="silu")
+    assert list(y.shape) == [1, m, n], y.shape
+    want = torch.nn.functional.silu(ref(x, held(tw, n)).double()).float()
+    check(f"linear rank 3 with silu rows {m}", y.float().cpu().reshape(m, n), want)
+
+
+@pytest.mark.parametrize("fmt", ["bfp8", "bfp4", "bf16"])
+def test_rows_each_pass_width(device, fmt):
+    """Every rows-per-pass width (1, 2, 4, 8 and passes of 8) of every format, on a K that is not a multiple of the
+    k-block (the padded values must not enter)."""
+    k, n = 800, 320
+    wt = _special(n, k, 40)
+    tw, _ = linear.native_weight(device, wt, DTYPES[fmt])
+    wk = held(tw, n)
+    for m in (1, 2, 3, 5, 8, 13):
+        x, tx = x_input(device, m, k, 50 + m)
+        check(f"{fmt} K {k} rows {m}", host(linear.matmul(tx, tw, None), m, n), ref(x, wk))
+
+
+def test_topk_merge(device):
+    k, n, rows, kk = 512, 4096, 4, 8
+    x, tx = x_input(device, 4, k, 60)
+    tw, _ = linear.native_weight(device, matrix(n, k, 61), linear.bfloat8_b)
+    for fp32 in (False, True):
+        r = linear.topk_result(device, linear.topk_slots(n), rows, kk)
+        spec = {"r": r, "k": kk, "rows": rows, "slot0": 0, "base": 0, "n": n, "write_y": True, "fp32": fp32}
+        y = linear.matmul(tx, tw, None, topk=spec)
+        vals, ids = linear.topk_merge(r, rows, kk, k_out=32, fp32=fp32)
+        hv, hi = linear.topk_records(r, rows, kk, fp32=fp32)
+        wv, wi = O.global_topk(hv.numpy(), hi.numpy(), 32)
+        same(f"global top-32 values (fp32 {fp32})", vals.cpu(), torch.from_numpy(wv))
+        same(f"global top-32 ids (fp32 {fp32})", ids.cpu().long(), torch.from_numpy(wi))
+        if not fp32:
+            yv = host(y, rows, n)
+            same("global top-32 against torch.topk of y", vals.cpu(), torch.topk(yv, 32, dim=1).values)

@@ -1,0 +1,145 @@
+"""Host-side checks that need no GPU: the C ABI library loads and exports every symbol include/dense_reader.h
+declares, its structs have the C layout, the planner and argument checks answer without touching a device, and the
+Python surface refuses what the reference refuses with the same exception types."""
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from dense_reader import _lib, linear
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "dense_reader.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(dr_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    names = _declared()
+    assert set(names) == set(_lib.SYMBOLS), (names, _lib.SYMBOLS)
+    for s in names:
+        assert hasattr(lib, s), s
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True).stdout
+    for s in names:
+        assert re.search(rf"\bT {s}\b", out), s
+
+
+def test_struct_layout_matches_c(tmp_path):
+    src = tmp_path / "layout.c"
+    src.write_text(
+        '#include <stdio.h>\n#include <stddef.h>\n#include "dense_reader.h"\n'
+        "int main(void){printf(\"%zu %zu %zu %zu %zu %zu %zu %zu\\n\", sizeof(dr_segment), sizeof(dr_topk),"
+        " sizeof(dr_launch), offsetof(dr_launch, seg), offsetof(dr_launch, topk), offsetof(dr_launch, stream),"
+        " offsetof(dr_topk, base), offsetof(dr_segment, col0));return 0;}\n"
+    )
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
+    got = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    want = [
+        ctypes.sizeof(_lib.Segment),
+        ctypes.sizeof(_lib.TopK),
+        ctypes.sizeof(_lib.Launch),
+        _lib.Launch.seg.offset,
+        _lib.Launch.topk.offset,
+        _lib.Launch.stream.offset,
+        _lib.TopK.base.offset,
+        _lib.Segment.col0.offset,
+    ]
+    assert got == want
+
+
+def test_plan_depends_on_k_only():
+    lib = _lib.lib()
+    assert lib.dr_version() >= 1
+    for k in (32, 1024, 2048, 4096, 14336):
+        c, kch, _ = _lib.plan(k, 1)
+        assert 1 <= c <= 16 and kch % 128 == 0 and c * kch >= k and (c - 1) * kch < -(-k // 128) * 128
+        for m in (2, 8, 32):
+            assert _lib.plan(k, m)[:2] == (c, kch)
+    assert _lib.plan(4096, 1)[2] == 1 and _lib.plan(4096, 3)[2] == 4 and _lib.plan(4096, 32)[2] == 8
+
+
+def test_sizes():
+    lib = _lib.lib()
+    assert lib.dr_codes_bytes(0, 256, 64) == 256 * 64
+    assert lib.dr_codes_bytes(1, 256, 64) == 256 * 32
+    assert lib.dr_codes_bytes(2, 256, 64) == 256 * 128
+    assert lib.dr_exps_bytes(0, 256, 64) == 256 * 4 and lib.dr_exps_bytes(2, 256, 64) == 0
+
+
+def test_invalid_arguments_refused_on_the_host():
+    lib = _lib.lib()
+    L = _lib.Launch()  # every pointer NULL
+    assert lib.dr_matmul(ctypes.byref(L)) == _lib.DR_EINVAL
+    L.x, L.y, L.m, L.k, L.ldx, L.nseg = 8, 8, 1, 48, 48, 1  # K not a multiple of 32
+    assert lib.dr_matmul(ctypes.byref(L)) == _lib.DR_EINVAL
+    L.k = L.ldx = 64
+    L.seg[0].fmt = 7  # no such format
+    assert lib.dr_matmul(ctypes.byref(L)) == _lib.DR_EINVAL
+    assert lib.dr_pack(None, 0, 0, 0, 0, None, None, None, 0, 0, None) == _lib.DR_EINVAL
+    assert lib.dr_topk_merge(None, 1, 1, 1, 0, 65, None, None, None) == _lib.DR_EINVAL
+    with pytest.raises(ValueError):
+        _lib.check(_lib.DR_EINVAL, "x")
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.DR_EHIP, "x")
+
+
+class _FakeWeight:
+    def __init__(self, k, n, dtype=linear.bfloat8_b, banks=8):
+        self.dtype = dtype
+        self.shape = (1, 1, k, n)
+        self.padded_shape = (1, 1, k, n)
+        self._mc = linear.MemoryConfig(banks, n // banks)
+
+    def memory_config(self):
+        return self._mc
+
+
+def test_block_list_rules():
+    a, b = _FakeWeight(1024, 256), _FakeWeight(1024, 512)
+    assert linear.is_block_list([(a, 0), (b, 8)])
+    assert not linear.is_block_list((a, b))  # linear's (gate, up) pair
+    assert not linear.is_block_list([(a, 0)])
+    assert not linear.is_block_list([(a, True), (b, 8)])
+    assert linear.is_block_list([(a, 0, None), (b, 8)])  # a per-block scale (beyond the reference)
+    with pytest.raises(AssertionError):
+        linear.block_entries([(a, 0), ((a, b), 8)])  # mixed plain and pairs
+    with pytest.raises(AssertionError):
+        linear.block_entries([(a, 0), (_FakeWeight(2048, 256), 8)])  # two K
+    assert len(linear.block_entries([(a, 0), (b, 8), (a, 24)])) == 3
+
+
+def test_check_banks_refuses_oversharded():
+    w = _FakeWeight(1024, 1024, banks=8)
+    linear.check_banks(w, 8)
+    with pytest.raises(ValueError):
+        linear.check_banks(w, 4)
+
+
+def test_records_host_decodes_the_reference_codec():
+    import torch
+
+    # two records of rows 1, k 2: keys of 1.0 (0x3F80 -> 0xBF80) and -2.0 (0xC000 -> 0x3FFF), an empty slot
+    t = torch.tensor([[0xBF80, 0x3FFF, 5, 7], [0, 0xBF80, -1, 9]], dtype=torch.int64).to(torch.int32)
+    vals, idx = linear.records_host(t, 1, 2)
+    assert vals.tolist() == [[1.0, -2.0, float("-inf"), 1.0]]
+    assert idx.tolist() == [[5, 7, -1, 9]]
+
+
+def test_interleave_and_bf16_ceil_match_oracle():
+    import torch
+
+    from oracle import dense_oracle as O
+
+    g = torch.randn(64, 32, generator=torch.Generator().manual_seed(1))
+    u = torch.randn(64, 32, generator=torch.Generator().manual_seed(2))
+    assert torch.equal(linear.interleave_glu(g, u), O.interleave_glu(g, u))
+    s = torch.rand(100, generator=torch.Generator().manual_seed(3)) + 1e-3
+    assert torch.equal(linear.bf16_ceil(s), O.bf16_ceil(s))

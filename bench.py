@@ -98,10 +98,10 @@ def main():
             spec = {"r": rec, "k": 8, "rows": m, "slot0": 0, "base": 0, "n": n, "write_y": False, "fp32": True}
             linear.matmul(x, ws[0], None, out=y, topk=spec)
             linear.topk_merge(rec, m, 8, k_out=32, fp32=True)
+        elif res is not None:
+            linear.matmul(x, ws[0], None, residual=res, out32=out32)  # (a residual takes a fresh output)
         else:
-            linear.matmul(x, ws[0], None, out=y, residual=res, out32=out32) if res is not None else linear.matmul(
-                x, ws[0], None, out=y, out32=out32
-            )
+            linear.matmul(x, ws[0], None, out=y, out32=out32)
 
     for i in range(a.warmup):
         call(i)

@@ -39,10 +39,11 @@ extern "C" {
 #define DR_ERANGE 3   /* a size beyond a documented limit */
 
 /* Geometry of a packed weight of K rows (in) and N columns (out):
- *   k_pad = K rounded up to 128, n_pad = N rounded up to 32 (or a multiple the caller asks for);
+ *   k_pad = K rounded up to 256, n_pad = N rounded up to 32 (or a multiple the caller asks for);
  *   codes: n_pad / 16 panels x k_pad values; bytes = k_pad * n_pad (bfp8), k_pad * n_pad / 2 (bfp4),
  *          2 * k_pad * n_pad (bf16);
- *   exps:  one byte per (panel, k): k_pad * n_pad / 16 bytes (bfp8, bfp4; none for bf16). */
+ *   exps:  one byte per (panel, k): k_pad * n_pad / 16 bytes (bfp8, bfp4; none for bf16), each panel's in groups
+ *          of 256 k ordered as the kernels read them (dense_reader.hip describes the layout). */
 int64_t dr_codes_bytes(int fmt, int k_pad, int n_pad);
 int64_t dr_exps_bytes(int fmt, int k_pad, int n_pad);
 

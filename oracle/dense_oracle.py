@@ -192,14 +192,27 @@ def held_exact(w, fmt):
 # --- the MI355X library's HBM layout (the packing the GPU kernels read) ------------------------------------------------
 
 KBLK = {"bfp8": 64, "bfp4": 128, "bf16": 32}
-KALIGN = 128
+
+
+def exp_off(fmt, k):
+    """The byte of a panel's exponents that holds k: groups of 256 k, byte 4 l + j of group g the j-th exponent lane l
+    of a wavefront reads (bfp8: k = 256 g + 64 j + l; bfp4: k = 256 g + 128 (j >> 1) + 32 kq + 2 i + (j & 1), with
+    l = 16 kq + i)."""
+    g, r = divmod(k, 256)
+    if fmt == "bfp8":
+        return g * 256 + 4 * (r & 63) + (r >> 6)
+    jb, r2 = divmod(r, 128)
+    kq, r3 = divmod(r2, 32)
+    i, h = divmod(r3, 2)
+    return g * 256 + 4 * (16 * kq + i) + 2 * jb + h
+KALIGN = 256
 
 
 def to_layout(w, fmt, n_pad=None):
     """The library's packed (codes, exps) for the float [K, N] matrix w, built from the reference-format tiles
     (bfp_tiles): panels of 16 columns, k-blocks of 1 KiB, lane l = 16 kq + c holding column c's values of the kq-th
     quarter; bfp8 int8 m, bfp4 nibbles u = m + 8 (byte j of dword d: k 8d + j low, 8d + 4 + j high), bf16 as is;
-    exponents one byte per (panel, k)."""
+    exponents one byte per (panel, k), placed by exp_off."""
     w = np.asarray(w.float().numpy() if isinstance(w, torch.Tensor) else w, np.float32)
     k, n = w.shape
     n_pad = n_pad or -(-n // 32) * 32
@@ -228,7 +241,11 @@ def to_layout(w, fmt, n_pad=None):
     sm = np.where(sgn == 1, -mag, mag).reshape(kt, nt, 2, 2, 16, 16)  # [KT, NT, fr, fc, r, c]
     sm = sm.transpose(0, 2, 4, 1, 3, 5).reshape(k_pad, n_pad)  # k = kt*32 + fr*16 + r, n = nt*32 + fc*16 + c
     ex = head.transpose(0, 2, 4, 1, 3).reshape(k_pad, nt * 2)  # [k, panel]
-    exps = np.ascontiguousarray(ex.T).reshape(-1).astype(np.uint8)  # panel-major, k order
+    # panel-major; within a panel, groups of 256 k with byte 4 l + j the j-th exponent lane l reads (exp_off)
+    perm = np.array([exp_off(fmt, kk) for kk in range(k_pad)], np.int64)
+    exps = np.zeros((npan, k_pad), np.uint8)
+    exps[:, perm] = ex.T
+    exps = exps.reshape(-1)
     if fmt == "bfp8":
         v = (sm & 0xFF).astype(np.uint8).reshape(nkb, 4, 16, npan, 16)  # k = b*64 + kq*16 + i
         codes = v.transpose(3, 0, 1, 4, 2).reshape(-1)

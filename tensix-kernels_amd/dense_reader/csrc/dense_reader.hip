@@ -8,12 +8,15 @@
 //   bfp4  (128 k a block): 32 k of column c; dword d holds k 8d .. 8d+7, byte j the nibbles (k 8d+j low, 8d+4+j
 //                          high), each u = m + 8 (offset binary, m in -7 .. 7);
 //   bf16  (32 k a block):  8 k of column c, the bf16 values.
-// The exponents sit apart: one byte per (panel, k), in k order (panel p at exps + p * k_pad). K is padded to 128 and
-// N to 32 (or what the caller asks); padding holds zeros (m = 0).
+// The exponents sit apart, one byte per (panel, k), panel p at exps + p * k_pad, in groups of 256 k: byte 4 l + j of
+// group g is the one lane l needs for the j-th of its four block-float k of that group (bfp8: k = 256 g + 64 j + l;
+// bfp4: the pair k = 256 g + 128 (j >> 1) + 32 kq + 2 i + (j & 1), l = 16 kq + i), so a lane reads one dword of
+// exponents per 256 k. K is padded to 256 and N to 32 (or what the caller asks); padding holds zeros (m = 0).
 //
-// The matmul (dr_gemv) gives each 32-column output tile one workgroup of `chunks` wavefronts; wavefront w sums the
-// tile's panels over one K chunk, and the chunks' partial sums are added in chunk order. The split depends on K only,
-// so every weight of one K sees the same sums in the same order: a block list equals one call per block bit for bit,
+// The matmul (dr_gemv) gives each 32-column output tile one workgroup. K is cut into chunks of 256 or 512 values (by
+// K alone); a wavefront sums the tile's panels over one chunk at a time, with every load of the chunk in flight at
+// once, and the chunks' partial sums are added in chunk order. The split depends on K only, so every weight of one K
+// sees the same sums in the same order: a block list equals one call per block bit for bit,
 // and repeated calls are bit-identical. Decode stays in registers: the block-float exponent of (k, panel) is folded
 // into x once per (k, panel) -- x * 2^(E - bias) is exact -- and broadcast across the 16 lanes of a row with DPP
 // row_newbcast, so each weight value costs one convert and one FMA (bfp8), or, for bfp4, half a byte permute and half
@@ -26,11 +29,20 @@
 
 namespace {
 
-constexpr int KALIGN = 128;  // K padding: a multiple of every format's k-block
-constexpr int MAXCH = 16;    // chunks (wavefronts) per output tile at most
+constexpr int KALIGN = 256;  // K padding: one exponent group; a multiple of every format's k-block
+constexpr int MAXW = 8;      // wavefronts a workgroup at most (512 threads: up to 256 VGPRs a lane)
+constexpr int LDS_MAX = 64 * 1024;  // the partial sums' LDS a workgroup at most
 constexpr int TILE = 32;
 
 __host__ __device__ constexpr int kblk(int fmt) { return fmt == DR_BFP8 ? 64 : (fmt == DR_BFP4 ? 128 : 32); }
+
+// the byte of a panel's exponents that holds k (see the layout above)
+__host__ __device__ constexpr int exp_off(int fmt, int k) {
+    const int g = k >> 8, r = k & 255;
+    if (fmt == DR_BFP8) return g * 256 + 4 * (r & 63) + (r >> 6);
+    const int jb = r >> 7, r2 = r & 127, kq = r2 >> 5, i = (r2 & 31) >> 1, h = r2 & 1;
+    return g * 256 + 4 * (16 * kq + i) + 2 * jb + h;
+}
 
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
 
@@ -41,15 +53,6 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
     uint32_t u = __float_as_uint(f);
     if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
     return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
-}
-
-template <int I>
-__device__ __forceinline__ float row_bcast(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + I, 0xF, 0xF, false));
-}
-template <int I>
-__device__ __forceinline__ uint32_t row_bcast_u(uint32_t v) {
-    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x150 + I, 0xF, 0xF, false);
 }
 
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
@@ -65,6 +68,7 @@ struct SegDev {
     const void* scale_up;
     int fmt, n, n_pad, glu, scale_f32, col0;
     int n_out, tiles, tile_begin;
+    unsigned pstride;  // bytes of codes a panel
 };
 
 struct Args {
@@ -80,164 +84,236 @@ struct Args {
     uint32_t* rec;
     int tk_k, tk_rows, slot0, n_valid, write_y, tk_fp32, row0;
     long long base;
-    int chunks, kch;
+    int chunks, kch, waves;
 };
 
-// ---- the K loop of one wavefront: partial sums of PW panels x MR rows over k-blocks [b0, b1) ----------------------
+// ---- the K loop of one wavefront: partial sums of PW panels x MR rows over [k0, k1) ------------------------------
+//
+// k0 and k1 are multiples of 256 (one exponent group: 4 bfp8 blocks, 2 bfp4 blocks, 8 bf16 blocks). Each group's
+// loads (PW 16-byte code loads a block, one exponent dword a panel, the x values) are all issued before any of them
+// is used and none sits under a branch, so a wavefront has a whole group in flight at once.
 
-// bfp8: lane (kq, c) accumulates column c over k = 64 b + 16 kq + i; lane (kq, i) makes x' for that k
+// acc += broadcast(s from lane I of this row of 16) * f, one VOP2 with DPP. The VALU write of s must be 2 wait states
+// before the DPP read of it: the first use of a fresh s carries an s_nop 1 (NOP = true).
+template <int I, bool NOP>
+__device__ __forceinline__ void fmac_bcast(float& acc, float s, float f) {
+    if constexpr (NOP)
+        asm volatile("s_nop 1\n\tv_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+                     : "+v"(acc) : "v"(s), "v"(f), "i"(I));
+    else
+        asm volatile("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+                     : "+v"(acc) : "v"(s), "v"(f), "i"(I));
+}
+
+// acc += dot(broadcast(bf16 pair p from lane J of this row of 16), bf16 pair a), one VOP2 with DPP (same hazard rule)
+template <int J, bool NOP>
+__device__ __forceinline__ void dot2_bcast(float& acc, uint32_t p, uint32_t a) {
+    if constexpr (NOP)
+        asm volatile("s_nop 1\n\tv_dot2c_f32_bf16_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+                     : "+v"(acc) : "v"(p), "v"(a), "i"(J));
+    else
+        asm volatile("v_dot2c_f32_bf16_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+                     : "+v"(acc) : "v"(p), "v"(a), "i"(J));
+}
+
+// a value the compiler cannot see through: masks made with it keep a load unconditional (a known-zero mask lets the
+// compiler put the load under a branch, and a load under a branch waits for every load before it)
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+// the bf16 bits of x[m][k], 0 for a row m or column k outside x (the load is clamped to valid memory, not skipped)
+__device__ __forceinline__ uint32_t x_bits(const Args& a, int m, int k) {
+    const int mc = min(m, a.m - 1), kc = min(k, a.k - 1);
+    const uint32_t v = a.x[(size_t)mc * a.ldx + kc];
+    return v & opaque((m < a.m && k < a.k) ? 0xFFFFFFFFu : 0u);
+}
+
+template <int PW>
+struct Codes {
+    uint4 c[PW];
+};
+
+template <int I, int MR, int PW>
+__device__ __forceinline__ void bfp8_step(float (&acc)[PW][MR], const float (&xs)[PW][MR], const uint4 (&c)[PW]) {
+#pragma unroll
+    for (int q = 0; q < PW; ++q) {
+        const uint32_t w = I / 4 == 0 ? c[q].x : I / 4 == 1 ? c[q].y : I / 4 == 2 ? c[q].z : c[q].w;
+        const float f = (float)(int)(signed char)(w >> (8 * (I % 4)));
+#pragma unroll
+        for (int m = 0; m < MR; ++m) fmac_bcast<I, I == 0>(acc[q][m], xs[q][m], f);
+    }
+    if constexpr (I + 1 < 16) bfp8_step<I + 1, MR, PW>(acc, xs, c);
+}
+
+// bfp8: lane (kq, c) accumulates column c over k = 64 b + 16 kq + i; lane (kq, i) makes x' for that k. One chunk
+// [k0, k1) of one or two exponent groups (256 k each): x first, then the exponents, then the codes are issued (waits
+// are in issue order, so x' is made before the codes arrive); a one-group chunk loads its group twice (the second
+// copy is never used) so that no load sits under a branch.
 template <int MR, int PW>
-__device__ __forceinline__ void loop_bfp8(const Args& a, const uint8_t* const* cb, const uint8_t* const* eb, int b0,
-                                          int b1, int lane, float (&acc)[PW][MR]) {
-    for (int b = b0; b < b1; b += 2) {
-        const bool two = b + 1 < b1;
-        uint4 c[2][PW];
-        int e[2][PW];
-        float xv[2][MR];
+__device__ __forceinline__ void chunk_bfp8(const Args& a, const uint8_t* const* cb, const uint8_t* const* eb, int k0,
+                                           int k1, int lane, float (&acc)[PW][MR]) {
+    const int g0 = k0 >> 8;
+    const bool two = k1 - k0 > 256;
+    const int g1 = two ? g0 + 1 : g0;
+    uint32_t xb[8][MR];
+    uint32_t e[2][PW];
+    Codes<PW> c[8];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int bb = (u == 0 || two) ? b + u : b;
+    for (int u = 0; u < 8; ++u) {
+        const int b = 4 * (u < 4 ? g0 : g1) + (u & 3);
 #pragma unroll
-            for (int q = 0; q < PW; ++q) {
-                c[u][q] = *reinterpret_cast<const uint4*>(cb[q] + (size_t)bb * 1024 + lane * 16);
-                e[u][q] = eb[q][bb * 64 + lane];
-            }
-            const int kx = bb * 64 + lane;
-#pragma unroll
-            for (int m = 0; m < MR; ++m) xv[u][m] = (kx < a.k && m < a.m) ? bf16_to_f32(a.x[(size_t)m * a.ldx + kx]) : 0.f;
-        }
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            if (u == 1 && !two) break;
-            float xs[PW][MR];
-#pragma unroll
-            for (int q = 0; q < PW; ++q)
-#pragma unroll
-                for (int m = 0; m < MR; ++m) xs[q][m] = __builtin_ldexpf(xv[u][m], e[u][q] - 133);
-            uint32_t w[PW][4];
-#pragma unroll
-            for (int q = 0; q < PW; ++q) {
-                w[q][0] = c[u][q].x;
-                w[q][1] = c[u][q].y;
-                w[q][2] = c[u][q].z;
-                w[q][3] = c[u][q].w;
-            }
-#define DR_STEP8(I)                                                                          \
-    {                                                                                        \
-        _Pragma("unroll") for (int q = 0; q < PW; ++q) {                                     \
-            const float f = (float)(int)(signed char)(w[q][(I) / 4] >> (8 * ((I) % 4)));     \
-            _Pragma("unroll") for (int m = 0; m < MR; ++m) acc[q][m] =                       \
-                __builtin_fmaf(row_bcast<(I)>(xs[q][m]), f, acc[q][m]);                      \
-        }                                                                                    \
+        for (int m = 0; m < MR; ++m) xb[u][m] = x_bits(a, m, b * 64 + lane);
     }
-            DR_STEP8(0) DR_STEP8(1) DR_STEP8(2) DR_STEP8(3) DR_STEP8(4) DR_STEP8(5) DR_STEP8(6) DR_STEP8(7)
-            DR_STEP8(8) DR_STEP8(9) DR_STEP8(10) DR_STEP8(11) DR_STEP8(12) DR_STEP8(13) DR_STEP8(14) DR_STEP8(15)
-#undef DR_STEP8
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int q = 0; q < PW; ++q)
+            e[h][q] = *reinterpret_cast<const uint32_t*>(eb[q] + (uint32_t)((h ? g1 : g0) * 256 + 4 * lane));
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const int b = 4 * (u < 4 ? g0 : g1) + (u & 3);
+#pragma unroll
+        for (int q = 0; q < PW; ++q) c[u].c[q] = *reinterpret_cast<const uint4*>(cb[q] + (uint32_t)(b * 1024 + lane * 16));
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        if (u == 4 && !two) break;
+        float xs[PW][MR];
+#pragma unroll
+        for (int q = 0; q < PW; ++q)
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+                xs[q][m] = __builtin_ldexpf(bf16_to_f32(xb[u][m]), (int)((e[u >> 2][q] >> (8 * (u & 3))) & 0xFFu) - 133);
+        bfp8_step<0, MR, PW>(acc, xs, c[u].c);
+    }
+}
+
+template <int D, int MR, int PW>
+__device__ __forceinline__ void bfp4_step(float (&acc)[PW][MR], const uint32_t (&xs)[PW][MR], const uint4 (&c)[PW]) {
+    constexpr uint32_t MAGIC = 0x43434343u;
+#pragma unroll
+    for (int q = 0; q < PW; ++q) {
+        const uint32_t w = D == 0 ? c[q].x : D == 1 ? c[q].y : D == 2 ? c[q].z : c[q].w;
+        const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+        // bf16 pairs 0x43uu: 128 + u = 136 + m, for k 8D + (0,1), (2,3) (low nibbles) and (4,5), (6,7) (high)
+        const uint32_t a0 = __builtin_amdgcn_perm(MAGIC, lo, 0x04010400u);
+        const uint32_t a1 = __builtin_amdgcn_perm(MAGIC, lo, 0x04030402u);
+        const uint32_t a2 = __builtin_amdgcn_perm(MAGIC, hi, 0x04010400u);
+        const uint32_t a3 = __builtin_amdgcn_perm(MAGIC, hi, 0x04030402u);
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            dot2_bcast<4 * D + 0, D == 0>(acc[q][m], xs[q][m], a0);
+            dot2_bcast<4 * D + 1, false>(acc[q][m], xs[q][m], a1);
+            dot2_bcast<4 * D + 2, false>(acc[q][m], xs[q][m], a2);
+            dot2_bcast<4 * D + 3, false>(acc[q][m], xs[q][m], a3);
         }
     }
+    if constexpr (D + 1 < 4) bfp4_step<D + 1, MR, PW>(acc, xs, c);
 }
 
 // bfp4: lane (kq, c) accumulates column c over k = 128 b + 32 kq + j (j < 32); lane (kq, i) makes the bf16 pair x'
 // for k = 128 b + 32 kq + 2i, +1. Weight values enter as bf16 136 + m (0x4300 | u), so acc = sum x' (136 + m) and
-// sx (per lane, the x' it made) gives the 136 * sum x' to take off.
+// sx (per lane, the x' it made) gives the 136 * sum x' to take off. One chunk of one or two exponent groups (two
+// blocks each), loaded as chunk_bfp8 loads its chunk.
 template <int MR, int PW>
-__device__ __forceinline__ void loop_bfp4(const Args& a, const uint8_t* const* cb, const uint8_t* const* eb, int b0,
-                                          int b1, int lane, float (&acc)[PW][MR], float (&sx)[PW][MR]) {
-    constexpr uint32_t MAGIC = 0x43434343u;
+__device__ __forceinline__ void chunk_bfp4(const Args& a, const uint8_t* const* cb, const uint8_t* const* eb, int k0,
+                                           int k1, int lane, float (&acc)[PW][MR], float (&sx)[PW][MR]) {
     const int kq = lane >> 4, i = lane & 15;
-    for (int b = b0; b < b1; b += 2) {
-        const bool two = b + 1 < b1;
-        uint4 c[2][PW];
-        uint32_t e[2][PW];
-        uint32_t xp[2][MR];
+    const int g0 = k0 >> 8;
+    const bool two = k1 - k0 > 256;
+    const int g1 = two ? g0 + 1 : g0;
+    uint32_t xp[4][MR];
+    uint32_t e[2][PW];
+    Codes<PW> c[4];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int bb = (u == 0 || two) ? b + u : b;
-            const int k0 = bb * 128 + kq * 32 + 2 * i;
+    for (int u = 0; u < 4; ++u) {
+        const int b = 2 * (u < 2 ? g0 : g1) + (u & 1);
+        const int kp = b * 128 + kq * 32 + 2 * i;
+        const int kc = min(kp, a.k - 2);  // (K is a multiple of 32: kp < K means kp + 1 < K)
 #pragma unroll
-            for (int q = 0; q < PW; ++q) {
-                c[u][q] = *reinterpret_cast<const uint4*>(cb[q] + (size_t)bb * 1024 + lane * 16);
-                e[u][q] = *reinterpret_cast<const uint16_t*>(eb[q] + k0);
-            }
-#pragma unroll
-            for (int m = 0; m < MR; ++m)
-                xp[u][m] = (k0 < a.k && m < a.m) ? *reinterpret_cast<const uint32_t*>(a.x + (size_t)m * a.ldx + k0) : 0u;
+        for (int m = 0; m < MR; ++m) {
+            const int mc = min(m, a.m - 1);
+            const uint32_t v = *reinterpret_cast<const uint32_t*>(a.x + (size_t)mc * a.ldx + kc);
+            xp[u][m] = v & opaque((kp < a.k && m < a.m) ? 0xFFFFFFFFu : 0u);
         }
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            if (u == 1 && !two) break;
-            uint32_t xs[PW][MR];
-#pragma unroll
-            for (int q = 0; q < PW; ++q)
-#pragma unroll
-                for (int m = 0; m < MR; ++m) {
-                    const float f0 = __builtin_ldexpf(bf16_to_f32(xp[u][m] & 0xFFFFu), (int)(e[u][q] & 0xFFu) - 129);
-                    const float f1 = __builtin_ldexpf(bf16_to_f32(xp[u][m] >> 16), (int)(e[u][q] >> 8) - 129);
-                    // exact: x has 8 significant bits, the power of two keeps them (a denormal result may lose
-                    // some; sx then takes the same truncated values the dot products see)
-                    const uint32_t p = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xFFFF0000u);
-                    xs[q][m] = p;
-                    sx[q][m] += bf16_to_f32(p & 0xFFFFu) + bf16_to_f32(p >> 16);
-                }
-#define DR_STEP4(D)                                                                                    \
-    {                                                                                                  \
-        _Pragma("unroll") for (int q = 0; q < PW; ++q) {                                               \
-            const uint32_t w = (D) == 0 ? c[u][q].x : (D) == 1 ? c[u][q].y : (D) == 2 ? c[u][q].z : c[u][q].w; \
-            const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;                          \
-            const uint32_t a0 = __builtin_amdgcn_perm(MAGIC, lo, 0x04010400u);                         \
-            const uint32_t a1 = __builtin_amdgcn_perm(MAGIC, lo, 0x04030402u);                         \
-            const uint32_t a2 = __builtin_amdgcn_perm(MAGIC, hi, 0x04010400u);                         \
-            const uint32_t a3 = __builtin_amdgcn_perm(MAGIC, hi, 0x04030402u);                         \
-            _Pragma("unroll") for (int m = 0; m < MR; ++m) {                                           \
-                acc[q][m] = dot2(a0, row_bcast_u<4 * (D) + 0>(xs[q][m]), acc[q][m]);                   \
-                acc[q][m] = dot2(a1, row_bcast_u<4 * (D) + 1>(xs[q][m]), acc[q][m]);                   \
-                acc[q][m] = dot2(a2, row_bcast_u<4 * (D) + 2>(xs[q][m]), acc[q][m]);                   \
-                acc[q][m] = dot2(a3, row_bcast_u<4 * (D) + 3>(xs[q][m]), acc[q][m]);                   \
-            }                                                                                          \
-        }                                                                                              \
     }
-            DR_STEP4(0) DR_STEP4(1) DR_STEP4(2) DR_STEP4(3)
-#undef DR_STEP4
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int q = 0; q < PW; ++q)
+            e[h][q] = *reinterpret_cast<const uint32_t*>(eb[q] + (uint32_t)((h ? g1 : g0) * 256 + 4 * lane));
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int b = 2 * (u < 2 ? g0 : g1) + (u & 1);
+#pragma unroll
+        for (int q = 0; q < PW; ++q) c[u].c[q] = *reinterpret_cast<const uint4*>(cb[q] + (uint32_t)(b * 1024 + lane * 16));
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        if (u == 2 && !two) break;
+        uint32_t xs[PW][MR];
+#pragma unroll
+        for (int q = 0; q < PW; ++q) {
+            const uint32_t ep = e[u >> 1][q] >> (16 * (u & 1));
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                const float f0 = __builtin_ldexpf(bf16_to_f32(xp[u][m] & 0xFFFFu), (int)(ep & 0xFFu) - 129);
+                const float f1 = __builtin_ldexpf(bf16_to_f32(xp[u][m] >> 16), (int)((ep >> 8) & 0xFFu) - 129);
+                // exact: x has 8 significant bits and a power of two keeps them (a denormal result may lose some;
+                // sx then adds the same truncated values the dot products see)
+                const uint32_t p = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xFFFF0000u);
+                xs[q][m] = p;
+                sx[q][m] += bf16_to_f32(p & 0xFFFFu) + bf16_to_f32(p >> 16);
+            }
         }
+        bfp4_step<0, MR, PW>(acc, xs, c[u].c);
     }
 }
 
 // bf16: lane (kq, c) accumulates column c over k = 32 b + 8 kq + j; x pairs are read as they are (the 16 lanes of a
 // row read the same 16 bytes)
 template <int MR, int PW>
-__device__ __forceinline__ void loop_bf16(const Args& a, const uint8_t* const* cb, int b0, int b1, int lane,
-                                          float (&acc)[PW][MR]) {
+__device__ __forceinline__ void chunk_bf16(const Args& a, const uint8_t* const* cb, int k0, int k1, int lane,
+                                           float (&acc)[PW][MR]) {
+    constexpr int G = 8 / PW;  // blocks a group (256 k is 8 blocks: 8 / G groups)
     const int kq = lane >> 4;
-    for (int b = b0; b < b1; b += 2) {
-        const bool two = b + 1 < b1;
-        uint4 c[2][PW];
-        uint4 xq[2][MR];
+    for (int gb = k0 / 32; gb < k1 / 32; gb += G) {
+        // x first, then the codes (waits are in issue order)
+        uint4 c[G][PW];
+        uint4 xq[G][MR];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int bb = (u == 0 || two) ? b + u : b;
+        for (int u = 0; u < G; ++u) {
+            const int b = gb + u;
+            const int kx = b * 32 + kq * 8;
+            const int kc = min(kx, a.k - 8);
 #pragma unroll
-            for (int q = 0; q < PW; ++q) c[u][q] = *reinterpret_cast<const uint4*>(cb[q] + (size_t)bb * 1024 + lane * 16);
-            const int k0 = bb * 32 + kq * 8;
-#pragma unroll
-            for (int m = 0; m < MR; ++m)
-                xq[u][m] = (k0 < a.k && m < a.m) ? *reinterpret_cast<const uint4*>(a.x + (size_t)m * a.ldx + k0)
-                                                 : make_uint4(0u, 0u, 0u, 0u);
+            for (int m = 0; m < MR; ++m) {
+                const int mc = min(m, a.m - 1);
+                const uint4 v = *reinterpret_cast<const uint4*>(a.x + (size_t)mc * a.ldx + kc);
+                const uint32_t keep = opaque((kx < a.k && m < a.m) ? 0xFFFFFFFFu : 0u);
+                xq[u][m] = make_uint4(v.x & keep, v.y & keep, v.z & keep, v.w & keep);
+            }
         }
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            if (u == 1 && !two) break;
+        for (int u = 0; u < G; ++u)
+#pragma unroll
+            for (int q = 0; q < PW; ++q)
+                c[u][q] = *reinterpret_cast<const uint4*>(cb[q] + (uint32_t)((gb + u) * 1024 + lane * 16));
+#pragma unroll
+        for (int u = 0; u < G; ++u)
 #pragma unroll
             for (int q = 0; q < PW; ++q)
 #pragma unroll
                 for (int m = 0; m < MR; ++m) {
-                    float s = acc[q][m];
-                    s = dot2(c[u][q].x, xq[u][m].x, s);
-                    s = dot2(c[u][q].y, xq[u][m].y, s);
-                    s = dot2(c[u][q].z, xq[u][m].z, s);
-                    s = dot2(c[u][q].w, xq[u][m].w, s);
-                    acc[q][m] = s;
+                    float v = acc[q][m];
+                    v = dot2(c[u][q].x, xq[u][m].x, v);
+                    v = dot2(c[u][q].y, xq[u][m].y, v);
+                    v = dot2(c[u][q].z, xq[u][m].z, v);
+                    v = dot2(c[u][q].w, xq[u][m].w, v);
+                    acc[q][m] = v;
                 }
-        }
     }
 }
 
@@ -259,23 +335,28 @@ __device__ __forceinline__ uint32_t key_f32(float f) {
     return u ^ ((u >> 31) ? 0xFFFFFFFFu : 0x80000000u);
 }
 
-template <int MR, int PW>
-__global__ __launch_bounds__(1024) void dr_gemv(const Args a) {
-    __shared__ float part[MAXCH][PW][MR][16];
+// FMT >= 0: every segment has that format (one K loop compiled in: a smaller kernel); FMT < 0: each workgroup
+// branches on its segment's format. ONE: a single segment.
+template <int MR, int PW, int FMT, bool ONE>
+__global__ __launch_bounds__(512) void dr_gemv(const Args a) {
+    extern __shared__ float part[];  // [chunks][PW][MR][16]: each chunk's column sums
     __shared__ float tval[MR][TILE];
     __shared__ uint32_t tkey[MR][TILE];
 
     const int g = blockIdx.x;
-    int s = 0;
+    int s = 0;  // (ONE: a single segment, found without reading the others' bounds first)
+    if (!ONE) {
 #pragma unroll
-    for (int j = 1; j < 4; ++j)
-        if (j < a.nseg && g >= a.seg[j].tile_begin) s = j;
+        for (int j = 1; j < 4; ++j)
+            if (j < a.nseg && g >= a.seg[j].tile_begin) s = j;
+    }
     const SegDev& sg = a.seg[s];
     const int t = g - sg.tile_begin;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int fmt = sg.fmt;
-    const int nkb = a.k_pad / kblk(fmt);
-    const size_t pstride = (size_t)nkb * 1024;
+    // (the wavefront index is uniform across the wavefront; readfirstlane lets the compiler see it, so the chunk
+    // bounds and loop trip counts live in SGPRs and the K loops branch on scalars)
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int fmt = FMT >= 0 ? FMT : sg.fmt;
+    const size_t pstride = sg.pstride;
 
     const uint8_t* cb[PW];
     const uint8_t* eb[PW];
@@ -299,48 +380,46 @@ __global__ __launch_bounds__(1024) void dr_gemv(const Args a) {
         eb[q] = ebase + (size_t)p * a.k_pad;
     }
 
-    float acc[PW][MR], corr[PW][MR];
-#pragma unroll
-    for (int q = 0; q < PW; ++q)
-#pragma unroll
-        for (int m = 0; m < MR; ++m) acc[q][m] = corr[q][m] = 0.f;
-
-    const int kb = kblk(fmt);
-    const int k0 = wave * a.kch, k1 = min(k0 + a.kch, a.k_pad);
-    const int b0 = k0 / kb, b1 = k1 / kb;
-    if (fmt == DR_BFP8) {
-        loop_bfp8<MR, PW>(a, cb, eb, b0, b1, lane, acc);
-    } else if (fmt == DR_BFP4) {
-        float sx[PW][MR];
+    for (int ch = wave; ch < a.chunks; ch += a.waves) {
+        float acc[PW][MR], corr[PW][MR];
 #pragma unroll
         for (int q = 0; q < PW; ++q)
 #pragma unroll
-            for (int m = 0; m < MR; ++m) sx[q][m] = 0.f;
-        loop_bfp4<MR, PW>(a, cb, eb, b0, b1, lane, acc, sx);
-        // the wavefront's 136 * sum x' (every lane made distinct x'), taken off every column
+            for (int m = 0; m < MR; ++m) acc[q][m] = corr[q][m] = 0.f;
+        const int k0 = ch * a.kch, k1 = min(k0 + a.kch, a.k_pad);
+        if (fmt == DR_BFP8) {
+            chunk_bfp8<MR, PW>(a, cb, eb, k0, k1, lane, acc);
+        } else if (fmt == DR_BFP4) {
+            float sx[PW][MR];
+#pragma unroll
+            for (int q = 0; q < PW; ++q)
+#pragma unroll
+                for (int m = 0; m < MR; ++m) sx[q][m] = 0.f;
+            chunk_bfp4<MR, PW>(a, cb, eb, k0, k1, lane, acc, sx);
+            // the wavefront's 136 * sum x' (every lane made distinct x'), taken off every column
+#pragma unroll
+            for (int q = 0; q < PW; ++q)
+#pragma unroll
+                for (int m = 0; m < MR; ++m) {
+                    float v = sx[q][m];
+#pragma unroll
+                    for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o);
+                    corr[q][m] = 136.f * v;
+                }
+        } else {
+            chunk_bf16<MR, PW>(a, cb, k0, k1, lane, acc);
+        }
+        // the chunk's column sums: the four quarter-rows of each column, in a fixed order
 #pragma unroll
         for (int q = 0; q < PW; ++q)
 #pragma unroll
             for (int m = 0; m < MR; ++m) {
-                float v = sx[q][m];
-#pragma unroll
-                for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o);
-                corr[q][m] = 136.f * v;
+                float v = acc[q][m];
+                v += __shfl_xor(v, 16);
+                v += __shfl_xor(v, 32);
+                if (lane < 16) part[((ch * PW + q) * MR + m) * 16 + lane] = v - corr[q][m];
             }
-    } else {
-        loop_bf16<MR, PW>(a, cb, b0, b1, lane, acc);
     }
-
-    // the wavefront's column sums: the four quarter-rows of each column, in a fixed order
-#pragma unroll
-    for (int q = 0; q < PW; ++q)
-#pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            float v = acc[q][m];
-            v += __shfl_xor(v, 16);
-            v += __shfl_xor(v, 32);
-            if (lane < 16) part[wave][q][m][lane] = v - corr[q][m];
-        }
     __syncthreads();
 
     // the epilogue: thread (m, col) of the 32-column output tile
@@ -356,8 +435,8 @@ __global__ __launch_bounds__(1024) void dr_gemv(const Args a) {
         if (PW == 4) {
             float gsum = 0.f, usum = 0.f;
             for (int w = 0; w < a.chunks; ++w) {
-                gsum += part[w][cq][m][cc];
-                usum += part[w][2 + cq][m][cc];
+                gsum += part[((w * PW + cq) * MR + m) * 16 + cc];
+                usum += part[((w * PW + 2 + cq) * MR + m) * 16 + cc];
             }
             float sgv = 1.f, suv = 1.f;
             if (valid) {
@@ -373,7 +452,7 @@ __global__ __launch_bounds__(1024) void dr_gemv(const Args a) {
         } else {
             const size_t ycol = (size_t)sg.col0 + oc;
             if (valid && a.res != nullptr && a.res_mode == 2) v = bf16_to_f32(a.res[(size_t)m * a.ldr + ycol]);
-            for (int w = 0; w < a.chunks; ++w) v += part[w][cq][m][cc];
+            for (int w = 0; w < a.chunks; ++w) v += part[((w * PW + cq) * MR + m) * 16 + cc];
             if (valid) {
                 v *= load_scale(sg.scale, sg.scale_f32, oc);
                 if (a.res != nullptr && a.res_mode == 1) v += bf16_to_f32(a.res[(size_t)m * a.ldr + ycol]);
@@ -504,8 +583,8 @@ __global__ __launch_bounds__(256) void dr_pack_k(const float* __restrict__ w, lo
     uint32_t ex[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) ex[i] = bfp_face_row<FMT == DR_BFP8 ? 7 : 3>(v[i], sm[i]);
-    *reinterpret_cast<uint2*>(exps + (size_t)p * k_pad + kk0) =
-        make_uint2(ex[0] | (ex[1] << 8) | (ex[2] << 16) | (ex[3] << 24), ex[4] | (ex[5] << 8) | (ex[6] << 16) | (ex[7] << 24));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) exps[(size_t)p * k_pad + exp_off(FMT, kk0 + i)] = (uint8_t)ex[i];
     if (FMT == DR_BFP8) {
         const int b = kk0 / 64, kq = (kk0 % 64) / 16, off = kk0 % 16;
 #pragma unroll
@@ -548,7 +627,7 @@ __global__ __launch_bounds__(256) void dr_unpack_k(const uint8_t* __restrict__ c
         const uint16_t h = *reinterpret_cast<const uint16_t*>(pbase + (size_t)b * 1024 + (kq * 16 + c) * 16 + 2 * i);
         val = bf16_to_f32(h);
     } else {
-        const int e = exps[(size_t)p * k_pad + kk];
+        const int e = exps[(size_t)p * k_pad + exp_off(FMT, kk)];
         int m;
         if (FMT == DR_BFP8) {
             const int b = kk / 64, kq = (kk % 64) / 16, i = kk % 16;
@@ -645,24 +724,42 @@ inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 int hip_status(hipError_t e) { return e == hipSuccess ? DR_OK : DR_EHIP; }
 
-void plan(int k, int* chunks, int* kch) {
+// the K range of one chunk: 512 (two exponent groups) from K = 4096 up, else 256 (more wavefronts for small K)
+#ifndef DR_CHUNK_K
+#define DR_CHUNK_K 0
+#endif
+
+void plan(int k, int* chunks, int* kch, int* waves) {
     const int k_pad = (k + KALIGN - 1) / KALIGN * KALIGN;
-    int c = (k_pad + 255) / 256;
-    if (c > MAXCH) c = MAXCH;
-    int ch = (k_pad + c - 1) / c;
-    ch = (ch + KALIGN - 1) / KALIGN * KALIGN;
+    const int ch = DR_CHUNK_K ? DR_CHUNK_K : (k_pad >= 4096 ? 512 : 256);
     *kch = ch;
     *chunks = (k_pad + ch - 1) / ch;
+    *waves = *chunks < MAXW ? *chunks : MAXW;
 }
 
 int rows_per_pass(int m) { return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8; }
 
+template <int MR, int PW>
+void launch_pw(const Args& a, int grid, hipStream_t st) {
+    const dim3 b(64 * a.waves);
+    const size_t lds = (size_t)a.chunks * PW * MR * 16 * sizeof(float);
+    if (a.nseg > 1) {
+        hipLaunchKernelGGL((dr_gemv<MR, PW, -1, false>), dim3(grid), b, lds, st, a);
+        return;
+    }
+    switch (a.seg[0].fmt) {
+        case DR_BFP8: hipLaunchKernelGGL((dr_gemv<MR, PW, DR_BFP8, true>), dim3(grid), b, lds, st, a); break;
+        case DR_BFP4: hipLaunchKernelGGL((dr_gemv<MR, PW, DR_BFP4, true>), dim3(grid), b, lds, st, a); break;
+        default: hipLaunchKernelGGL((dr_gemv<MR, PW, DR_BF16, true>), dim3(grid), b, lds, st, a); break;
+    }
+}
+
 template <int MR>
 hipError_t launch_mr(const Args& a, int pw, int grid, hipStream_t st) {
     if (pw == 2)
-        hipLaunchKernelGGL((dr_gemv<MR, 2>), dim3(grid), dim3(64 * a.chunks), 0, st, a);
-    else
-        hipLaunchKernelGGL((dr_gemv<MR, 4>), dim3(grid), dim3(64 * a.chunks), 0, st, a);
+        launch_pw<MR, 2>(a, grid, st);
+    else if constexpr (MR <= 4)  // (a GLU pass takes at most 4 rows: 8 would not fit the registers)
+        launch_pw<MR, 4>(a, grid, st);
     return hipGetLastError();
 }
 
@@ -715,8 +812,8 @@ int dr_unpack(const void* codes, const void* exps, int fmt, int n, int k, int n_
 
 int dr_plan(int k, int m, int32_t* chunks, int32_t* kch, int32_t* rpp) {
     if (k <= 0 || m <= 0) return DR_EINVAL;
-    int c, ch;
-    plan(k, &c, &ch);
+    int c, ch, w;
+    plan(k, &c, &ch, &w);
     if (chunks) *chunks = c;
     if (kch) *kch = ch;
     if (rpp) *rpp = rows_per_pass(m);
@@ -768,6 +865,7 @@ int dr_matmul(const dr_launch* L) {
         d.n_out = s.glu == 1 ? s.n / 2 : s.n;
         d.tiles = (d.n_out + TILE - 1) / TILE;
         d.tile_begin = tiles;
+        d.pstride = (unsigned)((a.k_pad / kblk(s.fmt)) * 1024);
         tiles += d.tiles;
         if ((int64_t)s.col0 + d.n_out > L->ldy) return DR_EINVAL;
     }
@@ -786,8 +884,13 @@ int dr_matmul(const dr_launch* L) {
         a.write_y = T.write_y != 0;
         a.tk_fp32 = T.fp32 != 0;
     }
-    plan(L->k, &a.chunks, &a.kch);
-    const int mr = rows_per_pass(L->m);
+    plan(L->k, &a.chunks, &a.kch, &a.waves);
+    int mr = rows_per_pass(L->m);
+    if (pw == 4 && mr > 4) mr = 4;
+    // (the partial sums of every chunk sit in LDS: fewer rows a pass when they would not fit; rows are independent,
+    // so this changes no result)
+    while (mr > 1 && (size_t)a.chunks * pw * mr * 16 * sizeof(float) > LDS_MAX) mr /= 2;
+    if ((size_t)a.chunks * pw * mr * 16 * sizeof(float) > LDS_MAX) return DR_ERANGE;
     hipStream_t st = S(L->stream);
     const size_t ysz = a.y_f32 ? 4 : 2;
     for (int r0 = 0; r0 < L->m; r0 += mr) {

@@ -48,7 +48,7 @@ from . import _lib  # noqa: E402
 
 BFP8_TILE = 1088
 NATIVE_TILES = {bfloat8_b: BFP8_TILE, bfloat4_b: 576, bfloat16: 2048}
-KALIGN = 128  # the packed layout pads K to this
+KALIGN = 256  # the packed layout pads K to this
 
 # --- settings (module attributes of the reference, linear.py:52-94) ---------------------------------------------------
 # The Tensix work-split knobs have no meaning on MI355X; they are kept so that code setting them runs, and, as in the

@@ -60,7 +60,8 @@ def test_plan_depends_on_k_only():
     assert lib.dr_version() >= 1
     for k in (32, 1024, 2048, 4096, 14336):
         c, kch, _ = _lib.plan(k, 1)
-        assert 1 <= c <= 16 and kch % 128 == 0 and c * kch >= k and (c - 1) * kch < -(-k // 128) * 128
+        k_pad = -(-k // 256) * 256
+        assert kch == (512 if k_pad >= 4096 else 256) and c == -(-k_pad // kch)
         for m in (2, 8, 32):
             assert _lib.plan(k, m)[:2] == (c, kch)
     assert _lib.plan(4096, 1)[2] == 1 and _lib.plan(4096, 3)[2] == 4 and _lib.plan(4096, 32)[2] == 8

@@ -113,6 +113,26 @@ def test_tile_topk_round_trip():
     assert np.all(np.diff(gv, axis=1) <= 0)
 
 
+def _eo(fmt, k):
+    """Exponent byte of k within a panel, from the layout's statement: groups of 256 k, lane l's four exponents at
+    bytes 4 l .. 4 l + 3, lane l making x' for (bfp8) k = 64 j + l, (bfp4) the pair 128 j' + 32 kq + 2 i (+1)."""
+    g, r = divmod(k, 256)
+    if fmt == "bfp8":
+        j, lane = divmod(r, 64)
+        return g * 256 + 4 * lane + j
+    jp, r = divmod(r, 128)
+    kq, r = divmod(r, 32)
+    i, h = divmod(r, 2)
+    return g * 256 + 4 * (16 * kq + i) + 2 * jp + h
+
+
+def test_exponent_layout_is_a_permutation():
+    for fmt in ("bfp8", "bfp4"):
+        offs = sorted(O.exp_off(fmt, k) for k in range(512))
+        assert offs == list(range(512))
+        assert all(O.exp_off(fmt, k) == _eo(fmt, k) for k in range(512))
+
+
 def _unlayout(codes, exps, fmt, k, n, n_pad):
     """Decode the library layout element by element with its address formula (independent of to_layout's
     reshapes)."""
@@ -127,14 +147,14 @@ def _unlayout(codes, exps, fmt, k, n, n_pad):
                 b, r = divmod(kk, 64)
                 kq, i = divmod(r, 16)
                 m = int(np.int8(codes[base + b * 1024 + (kq * 16 + cc) * 16 + i]))
-                out[kk, c] = np.ldexp(np.float32(m), int(exps[p * k_pad + kk]) - 133)
+                out[kk, c] = np.ldexp(np.float32(m), int(exps[p * k_pad + _eo('bfp8', kk)]) - 133)
             elif fmt == "bfp4":
                 b, r = divmod(kk, 128)
                 kq, r2 = divmod(r, 32)
                 d, j = divmod(r2, 8)
                 byte = int(codes[base + b * 1024 + (kq * 16 + cc) * 16 + d * 4 + (j & 3)])
                 u = (byte if j < 4 else byte >> 4) & 15
-                out[kk, c] = np.ldexp(np.float32(u - 8), int(exps[p * k_pad + kk]) - 129)
+                out[kk, c] = np.ldexp(np.float32(u - 8), int(exps[p * k_pad + _eo('bfp4', kk)]) - 129)
             else:
                 b, r = divmod(kk, 32)
                 kq, i = divmod(r, 8)
@@ -146,10 +166,10 @@ def _unlayout(codes, exps, fmt, k, n, n_pad):
 
 @pytest.mark.parametrize("fmt", ["bfp8", "bfp4", "bf16"])
 def test_layout_decodes_to_held(fmt):
-    k, n = 160, 48  # K padded to 256, N to 64
+    k, n = 288, 48  # K padded to 512, N to 64
     w = _special(k, n, 6)
     codes, exps = O.to_layout(w, fmt, n_pad=64)
-    assert codes.size * {"bfp8": 1, "bfp4": 2, "bf16": 0.5}[fmt] == 256 * 64
+    assert codes.size * {"bfp8": 1, "bfp4": 2, "bf16": 0.5}[fmt] == 512 * 64
     got = _unlayout(codes, exps, fmt, k, n, 64)
     assert np.array_equal(got, O.held(w, fmt))
 

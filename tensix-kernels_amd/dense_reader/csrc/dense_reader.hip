@@ -31,7 +31,6 @@ namespace {
 
 constexpr int KALIGN = 256;  // K padding: one exponent group; a multiple of every format's k-block
 constexpr int MAXW = 8;      // wavefronts a workgroup at most (512 threads: up to 256 VGPRs a lane)
-constexpr int LDS_MAX = 64 * 1024;  // the partial sums' LDS a workgroup at most
 constexpr int TILE = 32;
 
 __host__ __device__ constexpr int kblk(int fmt) { return fmt == DR_BFP8 ? 64 : (fmt == DR_BFP4 ? 128 : 32); }
@@ -335,31 +334,24 @@ __device__ __forceinline__ uint32_t key_f32(float f) {
     return u ^ ((u >> 31) ? 0xFFFFFFFFu : 0x80000000u);
 }
 
-// FMT >= 0: every segment has that format (one K loop compiled in: a smaller kernel); FMT < 0: each workgroup
-// branches on its segment's format. ONE: a single segment.
-template <int MR, int PW, int FMT, bool ONE>
-__global__ __launch_bounds__(512) void dr_gemv(const Args a) {
-    extern __shared__ float part[];  // [chunks][PW][MR][16]: each chunk's column sums
-    __shared__ float tval[MR][TILE];
-    __shared__ uint32_t tkey[MR][TILE];
+// ---- the workgroup's tile: its segment, its panels -------------------------------------------------------------------
 
-    const int g = blockIdx.x;
+template <bool ONE>
+__device__ __forceinline__ int find_segment(const Args& a, int g) {
     int s = 0;  // (ONE: a single segment, found without reading the others' bounds first)
     if (!ONE) {
 #pragma unroll
         for (int j = 1; j < 4; ++j)
             if (j < a.nseg && g >= a.seg[j].tile_begin) s = j;
     }
-    const SegDev& sg = a.seg[s];
-    const int t = g - sg.tile_begin;
-    // (the wavefront index is uniform across the wavefront; readfirstlane lets the compiler see it, so the chunk
-    // bounds and loop trip counts live in SGPRs and the K loops branch on scalars)
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int fmt = FMT >= 0 ? FMT : sg.fmt;
-    const size_t pstride = sg.pstride;
+    return s;
+}
 
-    const uint8_t* cb[PW];
-    const uint8_t* eb[PW];
+// the code and exponent bases of the tile's PW panels: plain weights the tile's two panels; interleave_glu weights the
+// gate tile's two panels then the up tile's; gate and up weights apart their tile's two panels each
+template <int PW>
+__device__ __forceinline__ void panel_ptrs(const SegDev& sg, int t, int k_pad, const uint8_t* (&cb)[PW],
+                                           const uint8_t* (&eb)[PW]) {
 #pragma unroll
     for (int q = 0; q < PW; ++q) {
         int p;
@@ -376,10 +368,129 @@ __global__ __launch_bounds__(512) void dr_gemv(const Args a) {
                 ebase = sg.exps_up;
             }
         }
-        cb[q] = cbase + (size_t)p * pstride;
-        eb[q] = ebase + (size_t)p * a.k_pad;
+        cb[q] = cbase + (size_t)p * sg.pstride;
+        eb[q] = ebase + (size_t)p * k_pad;
     }
+}
 
+// ---- the epilogue: the wavefronts' partial sums to the output stages ---------------------------------------------
+//
+// part [W][PW][ROWS][16]: wavefront w's column sums of panel q (the chunks it took, in order); they are added in w
+// order. Thread (m, col) of the 32-column output tile applies the scales, the GLU, the residual, writes y and keeps
+// the tile for the top-k ranking.
+template <int ROWS, int PW>
+__device__ __forceinline__ void epilogue(const Args& a, const SegDev& sg, int t, const float* part,
+                                         float (*tval)[TILE], uint32_t (*tkey)[TILE], int wave, int lane) {
+    const int mrows = min(a.m, ROWS);
+    const bool topk = a.rec != nullptr;
+    for (int e = threadIdx.x; e < TILE * ROWS; e += blockDim.x) {
+        const int m = e / TILE, col = e % TILE;
+        const int oc = t * TILE + col;  // output column of this segment
+        const bool valid = m < mrows && oc < sg.n_out;
+        float v = 0.f;
+        const int cq = col >> 4, cc = col & 15;
+        if (PW == 4) {
+            float gsum = 0.f, usum = 0.f;
+            for (int w = 0; w < a.waves; ++w) {
+                gsum += part[((w * PW + cq) * ROWS + m) * 16 + cc];
+                usum += part[((w * PW + 2 + cq) * ROWS + m) * 16 + cc];
+            }
+            float sgv = 1.f, suv = 1.f;
+            if (valid) {
+                if (sg.glu == 1) {
+                    sgv = load_scale(sg.scale, sg.scale_f32, 2 * t * TILE + col);
+                    suv = load_scale(sg.scale, sg.scale_f32, 2 * t * TILE + TILE + col);
+                } else {
+                    sgv = load_scale(sg.scale, sg.scale_f32, oc);
+                    suv = load_scale(sg.scale_up, sg.scale_f32, oc);
+                }
+            }
+            v = act_glu(gsum * sgv, a.act) * (usum * suv);
+        } else {
+            const size_t ycol = (size_t)sg.col0 + oc;
+            if (valid && a.res != nullptr && a.res_mode == 2) v = bf16_to_f32(a.res[(size_t)m * a.ldr + ycol]);
+            for (int w = 0; w < a.waves; ++w) v += part[((w * PW + cq) * ROWS + m) * 16 + cc];
+            if (valid) {
+                v *= load_scale(sg.scale, sg.scale_f32, oc);
+                if (a.res != nullptr && a.res_mode == 1) v += bf16_to_f32(a.res[(size_t)m * a.ldr + ycol]);
+            }
+        }
+        float out = v;
+        uint32_t ob = 0;
+        if (!a.y_f32) {
+            ob = f32_to_bf16(v);
+            out = bf16_to_f32(ob);
+        }
+        if (valid && (!topk || a.write_y)) {
+            const size_t idx = (size_t)m * a.ldy + sg.col0 + oc;
+            if (a.y_f32)
+                reinterpret_cast<float*>(a.y)[idx] = v;
+            else
+                reinterpret_cast<uint16_t*>(a.y)[idx] = (uint16_t)ob;
+        }
+        if (topk) {
+            const bool in = valid && oc < a.n_valid;
+            tval[m][col] = a.tk_fp32 ? v : out;
+            tkey[m][col] = !in ? 0u : (a.tk_fp32 ? key_f32(v) : key_bf16(ob));
+        }
+    }
+    if (!topk) return;
+    __syncthreads();
+    // one wavefront ranks each row's 32 keys: the best k, highest first, ties to the lower column
+    if (wave == 0) {
+        const int K = a.tk_k, R = a.tk_rows;
+        const size_t rlen = 2 * (size_t)R * K;
+        uint32_t* rec = a.rec + (size_t)(a.slot0 + t) * rlen;
+        for (int m = 0; m < mrows; ++m) {
+            const int r = a.row0 + m;
+            if (r >= R) break;
+            const int c = lane & 31;
+            const uint32_t key = tkey[m][c];
+            int rank = 0, nval = 0;
+            for (int j = 0; j < TILE; ++j) {
+                const uint32_t kj = tkey[m][j];
+                nval += kj != 0u;
+                rank += (kj > key) || (kj == key && j < c);
+            }
+            if (lane < 32 && key != 0u && rank < K) {
+                const float val = tval[m][c];
+                rec[(size_t)r * K + rank] = a.tk_fp32 ? __float_as_uint(val) : key;
+                rec[(size_t)R * K + (size_t)r * K + rank] = (uint32_t)(a.base + (long long)t * TILE + c);
+            }
+            if (lane >= nval && lane < K) {
+                rec[(size_t)r * K + lane] = a.tk_fp32 ? 0xFF800000u : 0u;
+                rec[(size_t)R * K + (size_t)r * K + lane] = 0xFFFFFFFFu;
+            }
+        }
+    }
+}
+
+// ---- the GEMV kernel (few rows): VALU decode and FMA, one accumulator a lane per panel and row -----------------------
+//
+// FMT >= 0: every segment has that format (one K loop compiled in: a smaller kernel); FMT < 0: each workgroup
+// branches on its segment's format. ONE: a single segment.
+template <int MR, int PW, int FMT, bool ONE>
+__global__ __launch_bounds__(512) void dr_gemv(const Args a) {
+    extern __shared__ float part[];  // [W][PW][MR][16]
+    __shared__ float tval[MR][TILE];
+    __shared__ uint32_t tkey[MR][TILE];
+
+    const int g = blockIdx.x;
+    const SegDev& sg = a.seg[find_segment<ONE>(a, g)];
+    const int t = g - sg.tile_begin;
+    // (the wavefront index is uniform across the wavefront; readfirstlane lets the compiler see it, so the chunk
+    // bounds and loop trip counts live in SGPRs and the K loops branch on scalars)
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int fmt = FMT >= 0 ? FMT : sg.fmt;
+    const uint8_t* cb[PW];
+    const uint8_t* eb[PW];
+    panel_ptrs<PW>(sg, t, a.k_pad, cb, eb);
+
+    float wsum[PW][MR];  // this wavefront's column sums (lanes 0..15), its chunks added in order
+#pragma unroll
+    for (int q = 0; q < PW; ++q)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) wsum[q][m] = 0.f;
     for (int ch = wave; ch < a.chunks; ch += a.waves) {
         float acc[PW][MR], corr[PW][MR];
 #pragma unroll
@@ -417,96 +528,272 @@ __global__ __launch_bounds__(512) void dr_gemv(const Args a) {
                 float v = acc[q][m];
                 v += __shfl_xor(v, 16);
                 v += __shfl_xor(v, 32);
-                if (lane < 16) part[((ch * PW + q) * MR + m) * 16 + lane] = v - corr[q][m];
+                wsum[q][m] += v - corr[q][m];
             }
     }
+    if (lane < 16) {
+#pragma unroll
+        for (int q = 0; q < PW; ++q)
+#pragma unroll
+            for (int m = 0; m < MR; ++m) part[((wave * PW + q) * MR + m) * 16 + lane] = wsum[q][m];
+    }
     __syncthreads();
+    epilogue<MR, PW>(a, sg, t, part, tval, tkey, wave, lane);
+}
 
-    // the epilogue: thread (m, col) of the 32-column output tile
-    const int tid = threadIdx.x;
-    const int mrows = min(a.m, MR);
-    const bool topk = a.rec != nullptr;
-    for (int e = tid; e < TILE * MR; e += blockDim.x) {
-        const int m = e / TILE, col = e % TILE;
-        const int oc = t * TILE + col;  // output column of this segment
-        const bool valid = m < mrows && oc < sg.n_out;
-        float v = 0.f;
-        const int cq = col >> 4, cc = col & 15;
-        if (PW == 4) {
-            float gsum = 0.f, usum = 0.f;
-            for (int w = 0; w < a.chunks; ++w) {
-                gsum += part[((w * PW + cq) * MR + m) * 16 + cc];
-                usum += part[((w * PW + 2 + cq) * MR + m) * 16 + cc];
+// ---- the MFMA kernel (rows in tiles of 16): 16x16x32 bf16 matrix cores, weights decoded to exact bf16 ---------------
+//
+// A is x (bf16 as it is: 16 rows of a row tile, 8 k a lane), B the weights: lane (kq, c) already holds column c at
+// consecutive k, the k-slots the MFMA wants, so B is its codes decoded in registers -- bf16 weights as they are,
+// block-float m * 2^(E - bias) (exact in bf16: at most 7 significant bits), the power of two broadcast across the row
+// from the lane that read that k's exponent. Output lane l: rows 4 (l / 16) .. +3 of column l % 16.
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+
+// d = broadcast(s from lane I of this row of 16) * f (the same hazard rule as fmac_bcast)
+template <int I, bool NOP>
+__device__ __forceinline__ float mul_bcast(float s, float f) {
+    float d;
+    if constexpr (NOP)
+        asm volatile("s_nop 1\n\tv_mul_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+                     : "=v"(d) : "v"(s), "v"(f), "i"(I));
+    else
+        asm volatile("v_mul_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+                     : "=v"(d) : "v"(s), "v"(f), "i"(I));
+    return d;
+}
+
+// two fp32 values with at most 8 significant bits as one bf16 pair (truncation is exact)
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+    return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
+// 16 bytes of x: row m, columns k .. k + 7 (k a multiple of 8). Rows past x read its last row: they only reach output
+// rows that are never written. Columns past K read its last columns and are zeroed by x_kmask (the weights there are
+// zero, but x might not be finite)
+__device__ __forceinline__ uint4 x_row8(const Args& a, int m, int k) {
+    const int mc = min(m, a.m - 1), kc = min(k, a.k - 8);
+    return *reinterpret_cast<const uint4*>(a.x + (size_t)mc * a.ldx + kc);
+}
+__device__ __forceinline__ void x_kmask(uint4& v, const Args& a, int k) {
+    if (k >= a.k) v = make_uint4(0u, 0u, 0u, 0u);
+}
+
+__device__ __forceinline__ f32x4 mfma(uint4 a, uint4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// B for 8 bfp8 values: bytes 8H .. 8H + 7 of the lane's codes (k-offsets 16 kq + 8H + j), times the broadcast scales
+template <int H>
+__device__ __forceinline__ uint4 b_bfp8(const uint4& w, float s) {
+    const uint32_t w0 = H ? w.z : w.x, w1 = H ? w.w : w.y;
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = (float)(int)(signed char)(w0 >> (8 * j));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[4 + j] = (float)(int)(signed char)(w1 >> (8 * j));
+    float p[8];
+    p[0] = mul_bcast<8 * H + 0, H == 0>(s, v[0]);
+    p[1] = mul_bcast<8 * H + 1, false>(s, v[1]);
+    p[2] = mul_bcast<8 * H + 2, false>(s, v[2]);
+    p[3] = mul_bcast<8 * H + 3, false>(s, v[3]);
+    p[4] = mul_bcast<8 * H + 4, false>(s, v[4]);
+    p[5] = mul_bcast<8 * H + 5, false>(s, v[5]);
+    p[6] = mul_bcast<8 * H + 6, false>(s, v[6]);
+    p[7] = mul_bcast<8 * H + 7, false>(s, v[7]);
+    return make_uint4(pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]), pack_bf16(p[4], p[5]), pack_bf16(p[6], p[7]));
+}
+
+// bfp8, one exponent group (4 blocks of 64 k): MFMA h of block b takes k = 64 b + 16 kq + 8 h + j
+template <int MT, int PW>
+__device__ __forceinline__ void mgroup_bfp8(const Args& a, const uint8_t* const* cb, const uint8_t* const* eb, int g,
+                                            int lane, f32x4 (&acc)[PW][MT]) {
+    const int r = lane & 15, kq = lane >> 4;
+    uint4 A[4][2][MT];
+    uint32_t e[PW];
+    uint4 c[4][PW];
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int tt = 0; tt < MT; ++tt) A[b][h][tt] = x_row8(a, 16 * tt + r, (4 * g + b) * 64 + 16 * kq + 8 * h);
+#pragma unroll
+    for (int q = 0; q < PW; ++q) e[q] = *reinterpret_cast<const uint32_t*>(eb[q] + (uint32_t)(g * 256 + 4 * lane));
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int q = 0; q < PW; ++q)
+            c[b][q] = *reinterpret_cast<const uint4*>(cb[q] + (uint32_t)((4 * g + b) * 1024 + lane * 16));
+    if (a.k != a.k_pad && (g + 1) * 256 > a.k) {  // (a ragged K's last group only)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int tt = 0; tt < MT; ++tt) x_kmask(A[b][h][tt], a, (4 * g + b) * 64 + 16 * kq + 8 * h);
+    }
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int q = 0; q < PW; ++q) {
+            // this lane's scale: the exponent of k = 64 b + lane (the lane whose index is that k's offset)
+            const float s = __builtin_ldexpf(1.f, (int)((e[q] >> (8 * b)) & 0xFFu) - 133);
+            const uint4 B0 = b_bfp8<0>(c[b][q], s);
+            const uint4 B1 = b_bfp8<1>(c[b][q], s);
+#pragma unroll
+            for (int tt = 0; tt < MT; ++tt) {
+                acc[q][tt] = mfma(A[b][0][tt], B0, acc[q][tt]);
+                acc[q][tt] = mfma(A[b][1][tt], B1, acc[q][tt]);
             }
-            float sgv = 1.f, suv = 1.f;
-            if (valid) {
-                if (sg.glu == 1) {
-                    sgv = load_scale(sg.scale, sg.scale_f32, 2 * t * TILE + col);
-                    suv = load_scale(sg.scale, sg.scale_f32, 2 * t * TILE + TILE + col);
-                } else {
-                    sgv = load_scale(sg.scale, sg.scale_f32, oc);
-                    suv = load_scale(sg.scale_up, sg.scale_f32, oc);
-                }
+        }
+}
+
+// B for the 8 bfp4 values of dword D (k-offsets 32 kq + 8 D + j): nibble u = m + 8 moved to the top of a byte with
+// its top bit flipped is 16 m as a signed byte; s0 / s1 carry 2^(E - 129) / 16 of the even / odd k of each pair,
+// broadcast from lane 4 D + j / 2
+template <int D>
+__device__ __forceinline__ uint4 b_bfp4(uint32_t w, float s0, float s1) {
+    const uint32_t lo = ((w << 4) & 0xF0F0F0F0u) ^ 0x80808080u;  // k 8D + 0..3
+    const uint32_t hi = (w & 0xF0F0F0F0u) ^ 0x80808080u;         // k 8D + 4..7
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = (float)(int)(signed char)(lo >> (8 * j));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[4 + j] = (float)(int)(signed char)(hi >> (8 * j));
+    float p[8];
+    p[0] = mul_bcast<4 * D + 0, D == 0>(s0, v[0]);
+    p[1] = mul_bcast<4 * D + 0, D == 0>(s1, v[1]);
+    p[2] = mul_bcast<4 * D + 1, false>(s0, v[2]);
+    p[3] = mul_bcast<4 * D + 1, false>(s1, v[3]);
+    p[4] = mul_bcast<4 * D + 2, false>(s0, v[4]);
+    p[5] = mul_bcast<4 * D + 2, false>(s1, v[5]);
+    p[6] = mul_bcast<4 * D + 3, false>(s0, v[6]);
+    p[7] = mul_bcast<4 * D + 3, false>(s1, v[7]);
+    return make_uint4(pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]), pack_bf16(p[4], p[5]), pack_bf16(p[6], p[7]));
+}
+
+// bfp4, one exponent group (2 blocks of 128 k): MFMA D of block b takes k = 128 b + 32 kq + 8 D + j
+template <int MT, int PW>
+__device__ __forceinline__ void mgroup_bfp4(const Args& a, const uint8_t* const* cb, const uint8_t* const* eb, int g,
+                                            int lane, f32x4 (&acc)[PW][MT]) {
+    const int r = lane & 15, kq = lane >> 4;
+    uint4 A[2][4][MT];
+    uint32_t e[PW];
+    uint4 c[2][PW];
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+#pragma unroll
+            for (int tt = 0; tt < MT; ++tt) A[b][d][tt] = x_row8(a, 16 * tt + r, (2 * g + b) * 128 + 32 * kq + 8 * d);
+#pragma unroll
+    for (int q = 0; q < PW; ++q) e[q] = *reinterpret_cast<const uint32_t*>(eb[q] + (uint32_t)(g * 256 + 4 * lane));
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int q = 0; q < PW; ++q)
+            c[b][q] = *reinterpret_cast<const uint4*>(cb[q] + (uint32_t)((2 * g + b) * 1024 + lane * 16));
+    if (a.k != a.k_pad && (g + 1) * 256 > a.k) {  // (a ragged K's last group only)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int d = 0; d < 4; ++d)
+#pragma unroll
+                for (int tt = 0; tt < MT; ++tt) x_kmask(A[b][d][tt], a, (2 * g + b) * 128 + 32 * kq + 8 * d);
+    }
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int q = 0; q < PW; ++q) {
+            // this lane's scales: the exponents of the pair k = 128 b + 32 kq + 2 i, + 1 (lane 16 kq + i)
+            const uint32_t ep = e[q] >> (16 * b);
+            const float s0 = __builtin_ldexpf(1.f, (int)(ep & 0xFFu) - 133);
+            const float s1 = __builtin_ldexpf(1.f, (int)((ep >> 8) & 0xFFu) - 133);
+            const uint4 B0 = b_bfp4<0>(c[b][q].x, s0, s1);
+            const uint4 B1 = b_bfp4<1>(c[b][q].y, s0, s1);
+            const uint4 B2 = b_bfp4<2>(c[b][q].z, s0, s1);
+            const uint4 B3 = b_bfp4<3>(c[b][q].w, s0, s1);
+#pragma unroll
+            for (int tt = 0; tt < MT; ++tt) {
+                acc[q][tt] = mfma(A[b][0][tt], B0, acc[q][tt]);
+                acc[q][tt] = mfma(A[b][1][tt], B1, acc[q][tt]);
+                acc[q][tt] = mfma(A[b][2][tt], B2, acc[q][tt]);
+                acc[q][tt] = mfma(A[b][3][tt], B3, acc[q][tt]);
             }
-            v = act_glu(gsum * sgv, a.act) * (usum * suv);
+        }
+}
+
+// bf16, 4 blocks of 32 k: the lane's 8 values are its B as they are (k = 32 b + 8 kq + j)
+template <int MT, int PW>
+__device__ __forceinline__ void mgroup_bf16(const Args& a, const uint8_t* const* cb, int b0, int lane,
+                                            f32x4 (&acc)[PW][MT]) {
+    const int r = lane & 15, kq = lane >> 4;
+    uint4 A[4][MT];
+    uint4 c[4][PW];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int tt = 0; tt < MT; ++tt) A[u][tt] = x_row8(a, 16 * tt + r, (b0 + u) * 32 + 8 * kq);
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int q = 0; q < PW; ++q) c[u][q] = *reinterpret_cast<const uint4*>(cb[q] + (uint32_t)((b0 + u) * 1024 + lane * 16));
+    if (a.k != a.k_pad && (b0 + 4) * 32 > a.k) {  // (a ragged K's last blocks only)
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int tt = 0; tt < MT; ++tt) x_kmask(A[u][tt], a, (b0 + u) * 32 + 8 * kq);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int q = 0; q < PW; ++q)
+#pragma unroll
+            for (int tt = 0; tt < MT; ++tt) acc[q][tt] = mfma(A[u][tt], c[u][q], acc[q][tt]);
+}
+
+template <int MT, int PW, int FMT, bool ONE>
+__global__ __launch_bounds__(512) void dr_mfma(const Args a) {
+    constexpr int ROWS = 16 * MT;
+    extern __shared__ float part[];  // [W][PW][ROWS][16]
+    __shared__ float tval[ROWS][TILE];
+    __shared__ uint32_t tkey[ROWS][TILE];
+
+    const int g = blockIdx.x;
+    const SegDev& sg = a.seg[find_segment<ONE>(a, g)];
+    const int t = g - sg.tile_begin;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int fmt = FMT >= 0 ? FMT : sg.fmt;
+    const uint8_t* cb[PW];
+    const uint8_t* eb[PW];
+    panel_ptrs<PW>(sg, t, a.k_pad, cb, eb);
+
+    f32x4 acc[PW][MT];  // this wavefront's sums over its chunks, in order
+#pragma unroll
+    for (int q = 0; q < PW; ++q)
+#pragma unroll
+        for (int tt = 0; tt < MT; ++tt) acc[q][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int ch = wave; ch < a.chunks; ch += a.waves) {
+        const int k0 = ch * a.kch, k1 = min(k0 + a.kch, a.k_pad);
+        if (fmt == DR_BFP8) {
+            for (int gg = k0 >> 8; gg < (k1 >> 8); ++gg) mgroup_bfp8<MT, PW>(a, cb, eb, gg, lane, acc);
+        } else if (fmt == DR_BFP4) {
+            for (int gg = k0 >> 8; gg < (k1 >> 8); ++gg) mgroup_bfp4<MT, PW>(a, cb, eb, gg, lane, acc);
         } else {
-            const size_t ycol = (size_t)sg.col0 + oc;
-            if (valid && a.res != nullptr && a.res_mode == 2) v = bf16_to_f32(a.res[(size_t)m * a.ldr + ycol]);
-            for (int w = 0; w < a.chunks; ++w) v += part[((w * PW + cq) * MR + m) * 16 + cc];
-            if (valid) {
-                v *= load_scale(sg.scale, sg.scale_f32, oc);
-                if (a.res != nullptr && a.res_mode == 1) v += bf16_to_f32(a.res[(size_t)m * a.ldr + ycol]);
-            }
-        }
-        float out = v;
-        uint32_t ob = 0;
-        if (!a.y_f32) {
-            ob = f32_to_bf16(v);
-            out = bf16_to_f32(ob);
-        }
-        if (valid && (!topk || a.write_y)) {
-            const size_t idx = (size_t)m * a.ldy + sg.col0 + oc;
-            if (a.y_f32)
-                reinterpret_cast<float*>(a.y)[idx] = v;
-            else
-                reinterpret_cast<uint16_t*>(a.y)[idx] = (uint16_t)ob;
-        }
-        if (topk) {
-            const bool in = valid && oc < a.n_valid;
-            tval[m][col] = a.tk_fp32 ? v : out;
-            tkey[m][col] = !in ? 0u : (a.tk_fp32 ? key_f32(v) : key_bf16(ob));
-            if (a.tk_fp32 && !in) tkey[m][col] = 0u;
+            for (int b0 = k0 / 32; b0 < k1 / 32; b0 += 4) mgroup_bf16<MT, PW>(a, cb, b0, lane, acc);
         }
     }
-    if (!topk) return;
+#pragma unroll
+    for (int q = 0; q < PW; ++q)
+#pragma unroll
+        for (int tt = 0; tt < MT; ++tt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                part[((wave * PW + q) * ROWS + 16 * tt + 4 * (lane >> 4) + j) * 16 + (lane & 15)] = acc[q][tt][j];
     __syncthreads();
-    // one wavefront ranks each row's 32 keys: the best k, highest first, ties to the lower column
-    if (wave == 0) {
-        const int K = a.tk_k, R = a.tk_rows;
-        const size_t rlen = 2 * (size_t)R * K;
-        uint32_t* rec = a.rec + (size_t)(a.slot0 + t) * rlen;
-        for (int m = 0; m < mrows; ++m) {
-            const int r = a.row0 + m;
-            if (r >= R) break;
-            const int c = lane & 31;
-            const uint32_t key = tkey[m][c];
-            int rank = 0, nval = 0;
-            for (int j = 0; j < TILE; ++j) {
-                const uint32_t kj = tkey[m][j];
-                nval += kj != 0u;
-                rank += (kj > key) || (kj == key && j < c);
-            }
-            if (lane < 32 && key != 0u && rank < K) {
-                const float val = tval[m][c];
-                rec[(size_t)r * K + rank] = a.tk_fp32 ? __float_as_uint(val) : key;
-                rec[(size_t)R * K + (size_t)r * K + rank] = (uint32_t)(a.base + (long long)t * TILE + c);
-            }
-            if (lane >= nval && lane < K) {
-                rec[(size_t)r * K + lane] = a.tk_fp32 ? 0xFF800000u : 0u;
-                rec[(size_t)R * K + (size_t)r * K + lane] = 0xFFFFFFFFu;
-            }
-        }
-    }
+    epilogue<ROWS, PW>(a, sg, t, part, tval, tkey, wave, lane);
 }
 
 // ---- packing ---------------------------------------------------------------------------------------------------------
@@ -737,12 +1024,20 @@ void plan(int k, int* chunks, int* kch, int* waves) {
     *waves = *chunks < MAXW ? *chunks : MAXW;
 }
 
-int rows_per_pass(int m) { return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8; }
+// the MFMA kernel from this many rows on; below it the GEMV kernel's rows a pass
+#ifndef DR_MFMA_MIN_M
+#define DR_MFMA_MIN_M 3
+#endif
+
+int rows_per_pass(int m) {
+    if (m >= DR_MFMA_MIN_M) return m <= 16 ? 16 : 32;
+    return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
+}
 
 template <int MR, int PW>
-void launch_pw(const Args& a, int grid, hipStream_t st) {
+void launch_gemv(const Args& a, int grid, hipStream_t st) {
     const dim3 b(64 * a.waves);
-    const size_t lds = (size_t)a.chunks * PW * MR * 16 * sizeof(float);
+    const size_t lds = (size_t)a.waves * PW * MR * 16 * sizeof(float);
     if (a.nseg > 1) {
         hipLaunchKernelGGL((dr_gemv<MR, PW, -1, false>), dim3(grid), b, lds, st, a);
         return;
@@ -754,12 +1049,31 @@ void launch_pw(const Args& a, int grid, hipStream_t st) {
     }
 }
 
-template <int MR>
-hipError_t launch_mr(const Args& a, int pw, int grid, hipStream_t st) {
-    if (pw == 2)
-        launch_pw<MR, 2>(a, grid, st);
-    else if constexpr (MR <= 4)  // (a GLU pass takes at most 4 rows: 8 would not fit the registers)
-        launch_pw<MR, 4>(a, grid, st);
+template <int MT, int PW>
+void launch_mfma(const Args& a, int grid, hipStream_t st) {
+    const dim3 b(64 * a.waves);
+    const size_t lds = (size_t)a.waves * PW * 16 * MT * 16 * sizeof(float);
+    if (a.nseg > 1) {
+        hipLaunchKernelGGL((dr_mfma<MT, PW, -1, false>), dim3(grid), b, lds, st, a);
+        return;
+    }
+    switch (a.seg[0].fmt) {
+        case DR_BFP8: hipLaunchKernelGGL((dr_mfma<MT, PW, DR_BFP8, true>), dim3(grid), b, lds, st, a); break;
+        case DR_BFP4: hipLaunchKernelGGL((dr_mfma<MT, PW, DR_BFP4, true>), dim3(grid), b, lds, st, a); break;
+        default: hipLaunchKernelGGL((dr_mfma<MT, PW, DR_BF16, true>), dim3(grid), b, lds, st, a); break;
+    }
+}
+
+// one pass of up to `rows` rows
+hipError_t launch_rows(const Args& a, int rows, int pw, int grid, hipStream_t st) {
+    switch (rows) {
+        case 1: pw == 2 ? launch_gemv<1, 2>(a, grid, st) : launch_gemv<1, 4>(a, grid, st); break;
+        case 2: pw == 2 ? launch_gemv<2, 2>(a, grid, st) : launch_gemv<2, 4>(a, grid, st); break;
+        case 4: pw == 2 ? launch_gemv<4, 2>(a, grid, st) : launch_gemv<4, 4>(a, grid, st); break;
+        case 8: launch_gemv<8, 2>(a, grid, st); break;  // (a GLU pass takes at most 4 GEMV rows)
+        case 16: pw == 2 ? launch_mfma<1, 2>(a, grid, st) : launch_mfma<1, 4>(a, grid, st); break;
+        default: launch_mfma<2, 2>(a, grid, st); break;  // (a GLU pass takes at most 16 MFMA rows)
+    }
     return hipGetLastError();
 }
 
@@ -886,11 +1200,8 @@ int dr_matmul(const dr_launch* L) {
     }
     plan(L->k, &a.chunks, &a.kch, &a.waves);
     int mr = rows_per_pass(L->m);
-    if (pw == 4 && mr > 4) mr = 4;
-    // (the partial sums of every chunk sit in LDS: fewer rows a pass when they would not fit; rows are independent,
-    // so this changes no result)
-    while (mr > 1 && (size_t)a.chunks * pw * mr * 16 * sizeof(float) > LDS_MAX) mr /= 2;
-    if ((size_t)a.chunks * pw * mr * 16 * sizeof(float) > LDS_MAX) return DR_ERANGE;
+    if (pw == 4 && mr == 8) mr = 4;    // (GLU: at most 4 GEMV rows or 16 MFMA rows a pass, for the registers
+    if (pw == 4 && mr == 32) mr = 16;  // and the LDS)
     hipStream_t st = S(L->stream);
     const size_t ysz = a.y_f32 ? 4 : 2;
     for (int r0 = 0; r0 < L->m; r0 += mr) {
@@ -901,13 +1212,7 @@ int dr_matmul(const dr_launch* L) {
         if (a.res) p.res = a.res + (size_t)r0 * a.ldr;
         p.row0 = r0;
         if (a.rec != nullptr && r0 >= a.tk_rows && !a.write_y) continue;
-        hipError_t e;
-        switch (mr) {
-            case 1: e = launch_mr<1>(p, pw, tiles, st); break;
-            case 2: e = launch_mr<2>(p, pw, tiles, st); break;
-            case 4: e = launch_mr<4>(p, pw, tiles, st); break;
-            default: e = launch_mr<8>(p, pw, tiles, st); break;
-        }
+        const hipError_t e = launch_rows(p, mr, pw, tiles, st);
         if (e != hipSuccess) return DR_EHIP;
     }
     return DR_OK;

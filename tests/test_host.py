@@ -64,7 +64,7 @@ def test_plan_depends_on_k_only():
         assert kch == (512 if k_pad >= 4096 else 256) and c == -(-k_pad // kch)
         for m in (2, 8, 32):
             assert _lib.plan(k, m)[:2] == (c, kch)
-    assert _lib.plan(4096, 1)[2] == 1 and _lib.plan(4096, 3)[2] == 4 and _lib.plan(4096, 32)[2] == 8
+    assert [_lib.plan(4096, m)[2] for m in (1, 2, 3, 16, 17, 32, 100)] == [1, 2, 16, 16, 32, 32, 32]
 
 
 def test_sizes():

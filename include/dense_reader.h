@@ -17,6 +17,8 @@
  *   dr_topk_merge  <- the host merge of top-k records, dense_reader/linear.py:747-768 (records_host) followed by a
  *                     best-k selection as lm_head_topk/lmhead.py:212-239 does on the host
  *   dr_plan        <- dense_reader/linear.py:455-495 choose/plan (the work split, for inspection only)
+ *   dr_workspace_bytes <- (no counterpart: the reference's per-core accumulators live in L1 circular buffers,
+ *                     linear.py:937; here a K split over workgroups meets in caller-provided device memory)
  */
 #ifndef DENSE_READER_H
 #define DENSE_READER_H
@@ -105,8 +107,15 @@ typedef struct dr_launch {
     int32_t nseg;        /* 1 .. 4 */
     dr_segment seg[4];
     dr_topk topk;
+    void* workspace;     /* device memory for split K (dr_workspace_bytes), zeroed once by the caller; or NULL */
+    int64_t workspace_bytes;
     void* stream;        /* hipStream_t */
 } dr_launch;
+
+/* Bytes of workspace the launch needs (0: none; a K long enough to split over several workgroups a tile needs some;
+ * -1: the launch is invalid). The workspace is zeroed once when allocated; every launch leaves its counters at zero.
+ * Launches that share one workspace must not overlap in time (one stream). */
+int64_t dr_workspace_bytes(const dr_launch* launch);
 
 /* y = the launch's fused matmul. Allocates nothing. */
 int dr_matmul(const dr_launch* launch);

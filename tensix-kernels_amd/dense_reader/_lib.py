@@ -20,6 +20,7 @@ SYMBOLS = (
     "dr_pack",
     "dr_unpack",
     "dr_matmul",
+    "dr_workspace_bytes",
     "dr_topk_merge",
     "dr_plan",
     "dr_status_string",
@@ -76,6 +77,8 @@ class Launch(ctypes.Structure):
         ("nseg", c_int32),
         ("seg", Segment * 4),
         ("topk", TopK),
+        ("workspace", c_void_p),
+        ("workspace_bytes", c_int64),
         ("stream", c_void_p),
     ]
 
@@ -104,6 +107,8 @@ def lib():
         L.dr_unpack.argtypes = [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_int64, c_void_p]
         L.dr_matmul.restype = c_int
         L.dr_matmul.argtypes = [ctypes.POINTER(Launch)]
+        L.dr_workspace_bytes.restype = c_int64
+        L.dr_workspace_bytes.argtypes = [ctypes.POINTER(Launch)]
         L.dr_topk_merge.restype = c_int
         L.dr_topk_merge.argtypes = [c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p]
         L.dr_plan.restype = c_int

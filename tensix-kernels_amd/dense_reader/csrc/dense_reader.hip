@@ -27,6 +27,10 @@
 
 #include "dense_reader.h"
 
+// No contraction of a multiply and an add into an FMA unless the code asks for one: the compiler would otherwise
+// decide per kernel instantiation, and a weight would round differently in a block list than alone.
+#pragma clang fp contract(off)
+
 namespace {
 
 constexpr int KALIGN = 256;  // K padding: one exponent group; a multiple of every format's k-block
@@ -84,6 +88,9 @@ struct Args {
     int tk_k, tk_rows, slot0, n_valid, write_y, tk_fp32, row0;
     long long base;
     int chunks, kch, waves;
+    int splits, cps, tiles;  // split K: splits workgroups a tile, cps chunks each; tiles of the launch
+    uint32_t* counters;      // [tiles] (splits > 1): workgroups of the tile done, reset to 0 by the last
+    float* wpart;            // [tiles][splits][PW * ROWS * 16] (splits > 1): each workgroup's column sums
 };
 
 // ---- the K loop of one wavefront: partial sums of PW panels x MR rows over [k0, k1) ------------------------------
@@ -375,11 +382,11 @@ __device__ __forceinline__ void panel_ptrs(const SegDev& sg, int t, int k_pad, c
 
 // ---- the epilogue: the wavefronts' partial sums to the output stages ---------------------------------------------
 //
-// part [W][PW][ROWS][16]: wavefront w's column sums of panel q (the chunks it took, in order); they are added in w
-// order. Thread (m, col) of the 32-column output tile applies the scales, the GLU, the residual, writes y and keeps
+// part [nparts][PW][ROWS][16]: column sums of panel q, added in order (the wavefronts', or with split K the
+// workgroups'). Thread (m, col) of the 32-column output tile applies the scales, the GLU, the residual, writes y and keeps
 // the tile for the top-k ranking.
 template <int ROWS, int PW>
-__device__ __forceinline__ void epilogue(const Args& a, const SegDev& sg, int t, const float* part,
+__device__ __forceinline__ void epilogue(const Args& a, const SegDev& sg, int t, const float* part, int nparts,
                                          float (*tval)[TILE], uint32_t (*tkey)[TILE], int wave, int lane) {
     const int mrows = min(a.m, ROWS);
     const bool topk = a.rec != nullptr;
@@ -391,7 +398,7 @@ __device__ __forceinline__ void epilogue(const Args& a, const SegDev& sg, int t,
         const int cq = col >> 4, cc = col & 15;
         if (PW == 4) {
             float gsum = 0.f, usum = 0.f;
-            for (int w = 0; w < a.waves; ++w) {
+            for (int w = 0; w < nparts; ++w) {
                 gsum += part[((w * PW + cq) * ROWS + m) * 16 + cc];
                 usum += part[((w * PW + 2 + cq) * ROWS + m) * 16 + cc];
             }
@@ -409,7 +416,7 @@ __device__ __forceinline__ void epilogue(const Args& a, const SegDev& sg, int t,
         } else {
             const size_t ycol = (size_t)sg.col0 + oc;
             if (valid && a.res != nullptr && a.res_mode == 2) v = bf16_to_f32(a.res[(size_t)m * a.ldr + ycol]);
-            for (int w = 0; w < a.waves; ++w) v += part[((w * PW + cq) * ROWS + m) * 16 + cc];
+            for (int w = 0; w < nparts; ++w) v += part[((w * PW + cq) * ROWS + m) * 16 + cc];
             if (valid) {
                 v *= load_scale(sg.scale, sg.scale_f32, oc);
                 if (a.res != nullptr && a.res_mode == 1) v += bf16_to_f32(a.res[(size_t)m * a.ldr + ycol]);
@@ -465,6 +472,38 @@ __device__ __forceinline__ void epilogue(const Args& a, const SegDev& sg, int t,
     }
 }
 
+// ---- split K: the tile's workgroups meet in the workspace ------------------------------------------------------------
+//
+// With splits > 1 each of a tile's workgroups takes cps chunks; it adds its wavefronts' sums (in order), writes them
+// to the workspace and counts itself done; the last one reads every workgroup's sums back, in split order, into part
+// and runs the epilogue (so the sum order is fixed: chunks within a wavefront, wavefronts within a split, splits), then
+// resets the tile's counter for the next launch. Returns the number of partial sums now in part, 0 when this
+// workgroup is not the tile's last.
+template <int ROWS, int PW>
+__device__ __forceinline__ int gather_splits(const Args& a, int g, int split, float* part) {
+    constexpr int E = PW * ROWS * 16;
+    __shared__ int last;
+    if (a.splits == 1) return a.waves;
+    float* mine = a.wpart + ((size_t)g * a.splits + split) * E;
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+        float v = 0.f;
+        for (int w = 0; w < a.waves; ++w) v += part[w * E + e];
+        mine[e] = v;
+    }
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(a.counters + g, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(a.splits - 1);
+    __syncthreads();
+    if (!last) return 0;
+    __threadfence();
+    const float* all = a.wpart + (size_t)g * a.splits * E;
+    for (int e = threadIdx.x; e < a.splits * E; e += blockDim.x) part[e] = __builtin_nontemporal_load(all + e);
+    if (threadIdx.x == 0) __hip_atomic_store(a.counters + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    return a.splits;
+}
+
 // ---- the GEMV kernel (few rows): VALU decode and FMA, one accumulator a lane per panel and row -----------------------
 //
 // FMT >= 0: every segment has that format (one K loop compiled in: a smaller kernel); FMT < 0: each workgroup
@@ -475,7 +514,7 @@ __global__ __launch_bounds__(512) void dr_gemv(const Args a) {
     __shared__ float tval[MR][TILE];
     __shared__ uint32_t tkey[MR][TILE];
 
-    const int g = blockIdx.x;
+    const int g = blockIdx.x % a.tiles, split = blockIdx.x / a.tiles;
     const SegDev& sg = a.seg[find_segment<ONE>(a, g)];
     const int t = g - sg.tile_begin;
     // (the wavefront index is uniform across the wavefront; readfirstlane lets the compiler see it, so the chunk
@@ -491,7 +530,8 @@ __global__ __launch_bounds__(512) void dr_gemv(const Args a) {
     for (int q = 0; q < PW; ++q)
 #pragma unroll
         for (int m = 0; m < MR; ++m) wsum[q][m] = 0.f;
-    for (int ch = wave; ch < a.chunks; ch += a.waves) {
+    const int ch1 = min((split + 1) * a.cps, a.chunks);
+    for (int ch = split * a.cps + wave; ch < ch1; ch += a.waves) {
         float acc[PW][MR], corr[PW][MR];
 #pragma unroll
         for (int q = 0; q < PW; ++q)
@@ -538,7 +578,8 @@ __global__ __launch_bounds__(512) void dr_gemv(const Args a) {
             for (int m = 0; m < MR; ++m) part[((wave * PW + q) * MR + m) * 16 + lane] = wsum[q][m];
     }
     __syncthreads();
-    epilogue<MR, PW>(a, sg, t, part, tval, tkey, wave, lane);
+    const int nparts = gather_splits<MR, PW>(a, g, split, part);
+    if (nparts) epilogue<MR, PW>(a, sg, t, part, nparts, tval, tkey, wave, lane);
 }
 
 // ---- the MFMA kernel (rows in tiles of 16): 16x16x32 bf16 matrix cores, weights decoded to exact bf16 ---------------
@@ -761,7 +802,7 @@ __global__ __launch_bounds__(512) void dr_mfma(const Args a) {
     __shared__ float tval[ROWS][TILE];
     __shared__ uint32_t tkey[ROWS][TILE];
 
-    const int g = blockIdx.x;
+    const int g = blockIdx.x % a.tiles, split = blockIdx.x / a.tiles;
     const SegDev& sg = a.seg[find_segment<ONE>(a, g)];
     const int t = g - sg.tile_begin;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -775,7 +816,8 @@ __global__ __launch_bounds__(512) void dr_mfma(const Args a) {
     for (int q = 0; q < PW; ++q)
 #pragma unroll
         for (int tt = 0; tt < MT; ++tt) acc[q][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int ch = wave; ch < a.chunks; ch += a.waves) {
+    const int ch1 = min((split + 1) * a.cps, a.chunks);
+    for (int ch = split * a.cps + wave; ch < ch1; ch += a.waves) {
         const int k0 = ch * a.kch, k1 = min(k0 + a.kch, a.k_pad);
         if (fmt == DR_BFP8) {
             for (int gg = k0 >> 8; gg < (k1 >> 8); ++gg) mgroup_bfp8<MT, PW>(a, cb, eb, gg, lane, acc);
@@ -793,7 +835,8 @@ __global__ __launch_bounds__(512) void dr_mfma(const Args a) {
             for (int j = 0; j < 4; ++j)
                 part[((wave * PW + q) * ROWS + 16 * tt + 4 * (lane >> 4) + j) * 16 + (lane & 15)] = acc[q][tt][j];
     __syncthreads();
-    epilogue<ROWS, PW>(a, sg, t, part, tval, tkey, wave, lane);
+    const int nparts = gather_splits<ROWS, PW>(a, g, split, part);
+    if (nparts) epilogue<ROWS, PW>(a, sg, t, part, nparts, tval, tkey, wave, lane);
 }
 
 // ---- packing ---------------------------------------------------------------------------------------------------------
@@ -1016,12 +1059,19 @@ int hip_status(hipError_t e) { return e == hipSuccess ? DR_OK : DR_EHIP; }
 #define DR_CHUNK_K 0
 #endif
 
-void plan(int k, int* chunks, int* kch, int* waves) {
+// a workgroup takes at most this many chunks; more K is split over several workgroups a tile
+#ifndef DR_SPLIT_CHUNKS
+#define DR_SPLIT_CHUNKS 8
+#endif
+
+void plan(int k, int* chunks, int* kch, int* waves, int* splits, int* cps) {
     const int k_pad = (k + KALIGN - 1) / KALIGN * KALIGN;
     const int ch = DR_CHUNK_K ? DR_CHUNK_K : (k_pad >= 4096 ? 512 : 256);
     *kch = ch;
     *chunks = (k_pad + ch - 1) / ch;
-    *waves = *chunks < MAXW ? *chunks : MAXW;
+    *splits = (*chunks + DR_SPLIT_CHUNKS - 1) / DR_SPLIT_CHUNKS;
+    *cps = (*chunks + *splits - 1) / *splits;
+    *waves = *cps < MAXW ? *cps : MAXW;
 }
 
 // the MFMA kernel from this many rows on; below it the GEMV kernel's rows a pass
@@ -1037,7 +1087,7 @@ int rows_per_pass(int m) {
 template <int MR, int PW>
 void launch_gemv(const Args& a, int grid, hipStream_t st) {
     const dim3 b(64 * a.waves);
-    const size_t lds = (size_t)a.waves * PW * MR * 16 * sizeof(float);
+    const size_t lds = (size_t)max(a.waves, a.splits) * PW * MR * 16 * sizeof(float);
     if (a.nseg > 1) {
         hipLaunchKernelGGL((dr_gemv<MR, PW, -1, false>), dim3(grid), b, lds, st, a);
         return;
@@ -1052,7 +1102,7 @@ void launch_gemv(const Args& a, int grid, hipStream_t st) {
 template <int MT, int PW>
 void launch_mfma(const Args& a, int grid, hipStream_t st) {
     const dim3 b(64 * a.waves);
-    const size_t lds = (size_t)a.waves * PW * 16 * MT * 16 * sizeof(float);
+    const size_t lds = (size_t)max(a.waves, a.splits) * PW * 16 * MT * 16 * sizeof(float);
     if (a.nseg > 1) {
         hipLaunchKernelGGL((dr_mfma<MT, PW, -1, false>), dim3(grid), b, lds, st, a);
         return;
@@ -1126,19 +1176,23 @@ int dr_unpack(const void* codes, const void* exps, int fmt, int n, int k, int n_
 
 int dr_plan(int k, int m, int32_t* chunks, int32_t* kch, int32_t* rpp) {
     if (k <= 0 || m <= 0) return DR_EINVAL;
-    int c, ch, w;
-    plan(k, &c, &ch, &w);
+    int c, ch, w, sp, cps;
+    plan(k, &c, &ch, &w, &sp, &cps);
     if (chunks) *chunks = c;
     if (kch) *kch = ch;
     if (rpp) *rpp = rows_per_pass(m);
     return DR_OK;
 }
 
-int dr_matmul(const dr_launch* L) {
+}  // extern "C"
+
+namespace {
+
+// the launch's arguments, its panel width, tiles and rows a pass (shared by dr_matmul and dr_workspace_bytes)
+int prepare(const dr_launch* L, Args& a, int& pw, int& tiles, int& mr) {
     if (L == nullptr || L->x == nullptr || L->y == nullptr || L->m <= 0 || L->k <= 0 || L->k % 32 ||
         L->ldx < L->k || L->nseg < 1 || L->nseg > 4)
         return DR_EINVAL;
-    Args a{};
     a.x = reinterpret_cast<const uint16_t*>(L->x);
     a.m = L->m;
     a.k = L->k;
@@ -1153,8 +1207,8 @@ int dr_matmul(const dr_launch* L) {
     a.act = L->act;
     if (a.act != 0 && a.act != 1) return DR_EINVAL;
     a.nseg = L->nseg;
-    const int pw = L->seg[0].glu ? 4 : 2;
-    int tiles = 0;
+    pw = L->seg[0].glu ? 4 : 2;
+    tiles = 0;
     for (int i = 0; i < L->nseg; ++i) {
         const dr_segment& s = L->seg[i];
         SegDev& d = a.seg[i];
@@ -1198,10 +1252,44 @@ int dr_matmul(const dr_launch* L) {
         a.write_y = T.write_y != 0;
         a.tk_fp32 = T.fp32 != 0;
     }
-    plan(L->k, &a.chunks, &a.kch, &a.waves);
-    int mr = rows_per_pass(L->m);
+    plan(L->k, &a.chunks, &a.kch, &a.waves, &a.splits, &a.cps);
+    a.tiles = tiles;
+    mr = rows_per_pass(L->m);
     if (pw == 4 && mr == 8) mr = 4;    // (GLU: at most 4 GEMV rows or 16 MFMA rows a pass, for the registers
     if (pw == 4 && mr == 32) mr = 16;  // and the LDS)
+    return DR_OK;
+}
+
+int64_t workspace_bytes(const Args& a, int pw, int mr) {
+    if (a.splits == 1) return 0;
+    const int64_t counters = ((int64_t)a.tiles * 4 + 255) / 256 * 256;
+    return counters + (int64_t)a.tiles * a.splits * pw * mr * 16 * 4;
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t dr_workspace_bytes(const dr_launch* L) {
+    Args a{};
+    int pw, tiles, mr;
+    if (prepare(L, a, pw, tiles, mr) != DR_OK) return -1;
+    return workspace_bytes(a, pw, mr);
+}
+
+int dr_matmul(const dr_launch* L) {
+    Args a{};
+    int pw, tiles, mr;
+    const int st0 = prepare(L, a, pw, tiles, mr);
+    if (st0 != DR_OK) return st0;
+    const int64_t need = workspace_bytes(a, pw, mr);
+    if (need > 0) {
+        // split K needs the workspace: its counters start at zero (the caller zeroes it once; each launch leaves
+        // them at zero)
+        if (L->workspace == nullptr || L->workspace_bytes < need) return DR_EINVAL;
+        a.counters = reinterpret_cast<uint32_t*>(L->workspace);
+        a.wpart = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(L->workspace) + (((int64_t)tiles * 4 + 255) / 256 * 256));
+    }
     hipStream_t st = S(L->stream);
     const size_t ysz = a.y_f32 ? 4 : 2;
     for (int r0 = 0; r0 < L->m; r0 += mr) {
@@ -1212,7 +1300,7 @@ int dr_matmul(const dr_launch* L) {
         if (a.res) p.res = a.res + (size_t)r0 * a.ldr;
         p.row0 = r0;
         if (a.rec != nullptr && r0 >= a.tk_rows && !a.write_y) continue;
-        const hipError_t e = launch_rows(p, mr, pw, tiles, st);
+        const hipError_t e = launch_rows(p, mr, pw, tiles * a.splits, st);
         if (e != hipSuccess) return DR_EHIP;
     }
     return DR_OK;

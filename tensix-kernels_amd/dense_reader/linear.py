@@ -488,9 +488,29 @@ def matmul(
         assert L.topk.slot0 + -(-n_out // TILE) <= L.topk.records_cap, (
             f"dense_reader: {-(-n_out // TILE)} records from slot {L.topk.slot0} do not fit {L.topk.records_cap}"
         )
-    L.stream = torch.cuda.current_stream(d).cuda_stream
+    st = torch.cuda.current_stream(d)
+    L.stream = st.cuda_stream
+    need = _lib.lib().dr_workspace_bytes(L)
+    _lib.check(_lib.DR_EINVAL if need < 0 else _lib.DR_OK, "dr_workspace_bytes")
+    if need > 0:
+        ws = _workspace(d, st, need)
+        L.workspace, L.workspace_bytes = ws.data_ptr(), ws.numel()
     _lib.check(_lib.lib().dr_matmul(L), "dr_matmul")
     return y
+
+
+_WORKSPACE = {}
+
+
+def _workspace(device, stream, nbytes):
+    """The split-K workspace of a device and stream: zeroed once when allocated (or grown); every launch leaves its
+    counters at zero, and launches on one stream never overlap."""
+    key = (device, stream.cuda_stream)
+    ws = _WORKSPACE.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _WORKSPACE[key] = ws
+    return ws
 
 
 def linear(x, w, scale, memory_config=None, activation=None, out_dtype=None, **opts):

@@ -273,3 +273,27 @@ def test_topk_merge(device):
         if not fp32:
             yv = host(y, rows, n)
             same("global top-32 against torch.topk of y", vals.cpu(), torch.topk(yv, 32, dim=1).values)
+
+
+@pytest.mark.parametrize("fmt", ["bfp8", "bfp4", "bf16"])
+def test_split_k(device, fmt):
+    """A K long enough to be split over several workgroups a tile (they meet in the workspace): against the oracle,
+    repeated calls bit-identical, a block list bit-identical to one call per block."""
+    n = 320
+    for k in (9216, 14336):
+        wt = matrix(n, k, 70)
+        tw, _ = linear.native_weight(device, wt, DTYPES[fmt])
+        tb, _ = linear.native_weight(device, matrix(256, k, 71), DTYPES[fmt])
+        wk = held(tw, n)
+        for m in (1, 3, 8):
+            x, tx = x_input(device, m, k, 72 + m)
+            y = linear.matmul(tx, tw, None)
+            check(f"{fmt} K {k} rows {m} (split K)", host(y, m, n), ref(x, wk))
+            same(f"{fmt} K {k} rows {m} repeated", host(linear.matmul(tx, tw, None), m, n), host(y, m, n))
+            one = linear.matmul(tx, [(tw, 0), (tb, 12)], None)
+            two = torch.zeros(1, 1, m, 12 * 32 + 256, dtype=torch.bfloat16, device=device.torch)
+            linear.matmul(tx, tw, None, out=two, col0=0)
+            linear.matmul(tx, tb, None, out=two, col0=12)
+            same(f"{fmt} K {k} rows {m} block list (split K)", host(one, m, 12 * 32 + 256)[:, :n],
+                 host(two, m, 12 * 32 + 256)[:, :n])
+            same(f"{fmt} K {k} rows {m} block list second block", host(one, m, 640)[:, 384:], host(two, m, 640)[:, 384:])

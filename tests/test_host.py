@@ -35,9 +35,9 @@ def test_struct_layout_matches_c(tmp_path):
     src = tmp_path / "layout.c"
     src.write_text(
         '#include <stdio.h>\n#include <stddef.h>\n#include "dense_reader.h"\n'
-        "int main(void){printf(\"%zu %zu %zu %zu %zu %zu %zu %zu\\n\", sizeof(dr_segment), sizeof(dr_topk),"
+        "int main(void){printf(\"%zu %zu %zu %zu %zu %zu %zu %zu %zu\\n\", sizeof(dr_segment), sizeof(dr_topk),"
         " sizeof(dr_launch), offsetof(dr_launch, seg), offsetof(dr_launch, topk), offsetof(dr_launch, stream),"
-        " offsetof(dr_topk, base), offsetof(dr_segment, col0));return 0;}\n"
+        " offsetof(dr_topk, base), offsetof(dr_segment, col0), offsetof(dr_launch, workspace_bytes));return 0;}\n"
     )
     exe = tmp_path / "layout"
     subprocess.run(["gcc", "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
@@ -51,6 +51,7 @@ def test_struct_layout_matches_c(tmp_path):
         _lib.Launch.stream.offset,
         _lib.TopK.base.offset,
         _lib.Segment.col0.offset,
+        _lib.Launch.workspace_bytes.offset,
     ]
     assert got == want
 

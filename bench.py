@@ -1,22 +1,29 @@
 """Benchmark of the dense_reader decode matmul on one MI355X.
 
-  python bench.py [--steps K] [--warmup W] [--config ns|c1|c2|c3|c4|c5] [--no-cpu]
+  python bench.py [--steps K] [--warmup W] [--config ns|c1|c2|c3|c4|c5] [--no-cpu] [--cpu-seconds S]
+  python bench.py --copy-probe      (a plain 256 MiB copy kernel: the byte counters' calibration under rocprofv3)
 
 Default workload: the north-star decode matmul, bfloat8_b M=1, x [1, 4096] bf16 @ W [4096 in, 14336 out] (W ~
-N(0, 0.02)), no fused stage, bf16 output. A step is one call. Weights rotate over enough distinct copies (>= 512 MB)
-that the 256 MB Infinity Cache cannot serve them; the K timed steps are captured once in a HIP graph and replayed
-(the analogue of the reference's ttnn trace), bracketed by synchronisation; each launch's own duration is also measured
-with HIP events around it on the stream it runs on (eager calls). One JSON line on stdout:
+N(0, 0.02)), no fused stage, bf16 output. A step is one call of the op (c5: the matmul with top-k records, then the
+merge of the records). Weights rotate over enough distinct copies (>= 512 MB) that the 256 MB Infinity Cache cannot
+serve them. The K timed steps are captured once in a HIP graph (the analogue of the reference's ttnn trace) and
+replayed between synchronisations; events on the replay stream bracket the timed region. One JSON line on stdout:
 
-  value = algorithmic weight bytes (the reference's 1088 B per bfloat8_b 32x32 tile) x steps / timed seconds, GB/s;
-  roofline.achieved = the same bytes per launch / the mean launch duration; cpu_baseline = the reference's torch CPU
-  check path (x in bf16 times the held weight in float32, dense_reader/linear.py:166-169) on this host's cores.
+  value             algorithmic weight bytes per step (the reference's 1088 / 576 / 2048 B per 32x32 tile of
+                    bfloat8_b / bfloat4_b / bfloat16) x steps / timed seconds, GB/s, inputs resident in HBM;
+  roofline.achieved the same bytes per matmul launch / that kernel's mean duration (a graph of K launches of the
+                    matmul alone, timed the same way; the step itself when it is one launch);
+  roofline.traffic  HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE runs (profiles/traffic.md), scaled by
+                    what the counters read for a copy kernel of known size, or null when no such row exists;
+  cpu_baseline      the reference's own float32 CPU check path (dense_reader/linear.py:166-169, restated in
+                    oracle.dense_oracle.ref_f32) with the config's epilogue, on this host's cores, on the same shapes.
 """
 
 import argparse
 import json
 import math
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -27,14 +34,35 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 MALL_BYTES = 512 * 2**20
+TRAFFIC_TABLE = ROOT / "profiles" / "traffic.md"
+METRIC = "weight GB/s and % HBM peak, bfp8_b M=1 decode matmul; µs/call"
 
+# name: (workload, m, k, weights [(n, fmt, scaled)], options)
 CONFIGS = {
-    # name: (description, m, k, n, fmt, options)
-    "ns": ("bfp8 M=1 K=4096 N=14336 decode matmul (north star)", 1, 4096, 14336, "bfp8", {}),
-    "c1": ("bfp8 M=1 K=2048 N=4096, no fused stage", 1, 2048, 4096, "bfp8", {}),
-    "c2": ("bfp4 M=1 K=4096 gate+up 2x14336, column scales, SwiGLU", 1, 4096, 14336, "bfp4", {"glu2": True, "scales": True}),
-    "c3": ("bfp8 M=8 K=14336 N=4096, residual, fp32 out", 8, 14336, 4096, "bfp8", {"residual": True, "out32": True}),
-    "c5": ("bfp8 M=4 K=4096 N=128256 LM head, top-8 per 32-column tile + global top-32", 4, 4096, 128256, "bfp8", {"topk": True}),
+    "ns": ("bfp8 M=1 K=4096 N=14336 decode matmul (north star)", 1, 4096, [(14336, "bfp8", False)], {}),
+    "c1": ("bfp8 M=1 K=2048 N=4096, no fused stage", 1, 2048, [(4096, "bfp8", False)], {}),
+    "c2": (
+        "bfp4 M=1 K=4096 gate+up 2x14336, fp32 column scales, SwiGLU",
+        1,
+        4096,
+        [(14336, "bfp4", True), (14336, "bfp4", True)],
+        {"glu2": True},
+    ),
+    "c3": ("bfp8 M=8 K=14336 N=4096, residual, fp32 out", 8, 14336, [(4096, "bfp8", False)], {"residual": True}),
+    "c4": (
+        "block list M=32 K=4096: Q 4096 + K 1024 + V 1024 bfp8 with column scales, O 4096 bf16, one launch",
+        32,
+        4096,
+        [(4096, "bfp8", True), (1024, "bfp8", True), (1024, "bfp8", True), (4096, "bf16", False)],
+        {"blocks": True},
+    ),
+    "c5": (
+        "bfp8 M=4 K=4096 N=128256 LM head, fp32 top-8 records per 32-column tile + global top-32 merge",
+        4,
+        4096,
+        [(128256, "bfp8", False)],
+        {"topk": True},
+    ),
 }
 
 
@@ -45,105 +73,155 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="ns", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--copy-probe", action="store_true")
     return ap.parse_args()
+
+
+def copy_probe():
+    """Five launches of one elementwise kernel that reads 256 MiB and writes 256 MiB (torch.neg, float32)."""
+    import torch
+
+    n = 64 * 2**20
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe": "torch.neg float32", "read_bytes": 4 * n, "write_bytes": 4 * n}), flush=True)
+
+
+def traffic_row(name):
+    """HBM bytes per matmul launch for config `name` from the table of profiles/traffic.md (a row
+    `| name | kernel | ... | bytes |` whose last cell is the scaled traffic), or None."""
+    if not TRAFFIC_TABLE.exists():
+        return None
+    for line in TRAFFIC_TABLE.read_text().splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 3 and cells[0] == name and re.fullmatch(r"\d+", cells[-1]):
+            return int(cells[-1])
+    return None
+
+
+class Workload:
+    """The inputs of one config on the GPU and its two launch sequences: step(i) (the op as a user calls it) and
+    kernel(i) (the matmul launch alone)."""
+
+    def __init__(self, name, linear, torch):
+        self.name = name
+        desc, m, k, ws, o = CONFIGS[name]
+        self.desc, self.m, self.k, self.spec, self.o = desc, m, k, ws, o
+        self.linear = linear
+        dev = linear.dev.open_device(0)
+        g = torch.Generator(device="cuda").manual_seed(0)
+        fmts = {"bfp8": linear.bfloat8_b, "bfp4": linear.bfloat4_b, "bf16": linear.bfloat16}
+        self.x = torch.randn(m, k, generator=g, device="cuda").to(torch.bfloat16).reshape(1, 1, m, k)
+
+        def make():
+            return [linear.native_weight(dev, torch.randn(n, k, generator=g, device="cuda") * 0.02, fmts[f])[0] for n, f, _ in ws]
+
+        first = make()
+        self.wbytes = sum(w.algorithmic_bytes() for w in first)
+        self.copies = max(2, math.ceil(MALL_BYTES / sum(w.nbytes() for w in first)) + 1)
+        self.sets = [first] + [make() for _ in range(self.copies - 1)]
+        self.scales = [
+            linear.scale_tensor(dev, torch.rand(n, generator=g, device="cuda") + 0.5, dtype=linear.float32) if sc else None
+            for n, _, sc in ws
+        ]
+        self.n = ws[0][0] if (o.get("glu2")) else sum(n for n, _, _ in ws)
+        n = self.n
+        self.res = torch.randn(m, n, generator=g, device="cuda").to(torch.bfloat16).reshape(1, 1, m, n) if o.get("residual") else None
+        self.y = torch.empty(1, 1, m, n, dtype=torch.bfloat16, device="cuda")
+        self.rec = linear.topk_result(dev, linear.topk_slots(n), m, 8) if o.get("topk") else None
+        self.col0 = []
+        c = 0
+        for nb, _, _ in ws:
+            self.col0.append(c // 32)
+            c += nb
+
+    def kernel(self, i):
+        L, o, ws = self.linear, self.o, self.sets[i % self.copies]
+        if o.get("glu2"):
+            L.matmul(self.x, ws[0], self.scales[0], out=self.y, glu=True, w_up=ws[1], scale_up=self.scales[1])
+        elif o.get("blocks"):
+            blocks = [(w, c0, s) if s is not None else (w, c0) for w, c0, s in zip(ws, self.col0, self.scales)]
+            L.matmul(self.x, blocks, None, out=self.y)
+        elif o.get("topk"):
+            spec = {"r": self.rec, "k": 8, "rows": self.m, "slot0": 0, "base": 0, "n": self.n, "write_y": False, "fp32": True}
+            L.matmul(self.x, ws[0], None, out=self.y, topk=spec)
+        elif self.res is not None:
+            L.matmul(self.x, ws[0], None, residual=self.res, out32=True)  # (fp32 out: a fresh output each call)
+        else:
+            L.matmul(self.x, ws[0], None, out=self.y)
+
+    def step(self, i):
+        self.kernel(i)
+        if self.o.get("topk"):
+            self.linear.topk_merge(self.rec, self.m, 8, k_out=32, fp32=True)
+
+
+def timed_graph(torch, fn, steps):
+    """ms for `steps` calls of fn captured in one HIP graph and replayed once (after one untimed replay), events on
+    the replay stream."""
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(steps):
+            fn(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(st)
+    graph.replay()
+    t1.record(st)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1)
 
 
 def main():
     a = parse()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(
-            "bench.py: this build measures one GPU; the decode matmul would shard its output columns over GPUs "
-            "(see DESIGN.md) and no multi-GPU figure is produced",
+            "bench.py: this build measures one GPU only; the decode matmul would shard its output columns over GPUs "
+            "and no figure at several GPUs is produced",
             file=sys.stderr,
         )
         sys.exit(2)
     import torch
 
+    if a.copy_probe:
+        copy_probe()
+        return
+
     from dense_reader import linear
 
-    name = a.config
-    desc, m, k, n, fmt, o = CONFIGS[name]
-    dtype = {"bfp8": linear.bfloat8_b, "bfp4": linear.bfloat4_b, "bf16": linear.bfloat16}[fmt]
-    dev = linear.dev.open_device(0)
-    g = torch.Generator(device="cuda").manual_seed(0)
-    x = torch.randn(m, k, generator=g, device="cuda").to(torch.bfloat16).reshape(1, 1, m, k)
-    nw = 2 if o.get("glu2") else 1
-
-    def make():
-        ws = [linear.native_weight(dev, torch.randn(n, k, generator=g, device="cuda") * 0.02, dtype)[0] for _ in range(nw)]
-        return ws
-
-    one = make()
-    wbytes = sum(w.algorithmic_bytes() for w in one)
-    copies = max(2, math.ceil(MALL_BYTES / sum(w.nbytes() for w in one)) + 1)
-    sets = [one] + [make() for _ in range(copies - 1)]
-    scales = None
-    if o.get("scales"):
-        scales = [linear.scale_tensor(dev, torch.rand(n, generator=g, device="cuda") + 0.5, dtype=linear.float32) for _ in range(nw)]
-    res = torch.randn(m, n, generator=g, device="cuda").to(torch.bfloat16).reshape(1, 1, m, n) if o.get("residual") else None
-    out32 = bool(o.get("out32"))
-    n_out = n
-    y = torch.empty(1, 1, m, n_out, dtype=torch.float32 if out32 else torch.bfloat16, device="cuda")
-    rec = None
-    if o.get("topk"):
-        rec = linear.topk_result(dev, linear.topk_slots(n), m, 8)
-        gv = torch.empty(m, 32, dtype=torch.float32, device="cuda")
-
-    def call(i):
-        ws = sets[i % copies]
-        if o.get("glu2"):
-            linear.matmul(x, ws[0], scales[0], out=y, glu=True, w_up=ws[1], scale_up=scales[1])
-        elif o.get("topk"):
-            spec = {"r": rec, "k": 8, "rows": m, "slot0": 0, "base": 0, "n": n, "write_y": False, "fp32": True}
-            linear.matmul(x, ws[0], None, out=y, topk=spec)
-            linear.topk_merge(rec, m, 8, k_out=32, fp32=True)
-        elif res is not None:
-            linear.matmul(x, ws[0], None, residual=res, out32=out32)  # (a residual takes a fresh output)
-        else:
-            linear.matmul(x, ws[0], None, out=y, out32=out32)
-
+    wl = Workload(a.config, linear, torch)
     for i in range(a.warmup):
-        call(i)
+        wl.step(i)
     torch.cuda.synchronize()
 
-    # each launch's own duration, eager, events on the launch stream
+    # eager: each call bracketed by events on its stream (host launch cost included)
     st = torch.cuda.current_stream()
     nev = min(a.steps, 100)
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(nev)]
     for i in range(nev):
         ev[i][0].record(st)
-        call(i)
+        wl.step(i)
         ev[i][1].record(st)
     torch.cuda.synchronize()
-    durs = sorted(e0.elapsed_time(e1) * 1e3 for e0, e1 in ev)  # us
-    mean_us = sum(durs) / len(durs)
-    med_us = durs[len(durs) // 2]
+    eager = sorted(e0.elapsed_time(e1) * 1e3 for e0, e1 in ev)
 
-    # the timed region: K steps captured in one graph, replayed between synchronisations
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for i in range(a.steps):
-            call(i)
-    graph.replay()
-    torch.cuda.synchronize()
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0.record()
-    graph.replay()
-    t1.record()
-    torch.cuda.synchronize()
-    total_ms = t0.elapsed_time(t1)
+    total_ms = timed_graph(torch, wl.step, a.steps)
     ms_per_step = total_ms / a.steps
-    value = wbytes * a.steps / (total_ms * 1e-3) / 1e9
-    achieved = wbytes / (mean_us * 1e-6) / 1e9
+    value = wl.wbytes * a.steps / (total_ms * 1e-3) / 1e9
+    kern_ms = total_ms if not wl.o.get("topk") else timed_graph(torch, wl.kernel, a.steps)
+    launch_us = kern_ms * 1e3 / a.steps
+    achieved = wl.wbytes / (launch_us * 1e-6) / 1e9
 
-    cpu = None
-    if not a.no_cpu:
-        cpu = cpu_baseline(linear, x, one, scales, res, o, m, n, wbytes, a.cpu_seconds)
-
+    cpu = None if a.no_cpu else cpu_baseline(wl, a.cpu_seconds)
+    fmts = sorted({f for _, f, _ in wl.spec})
     line = {
-        "metric": "weight GB/s and % HBM peak, bfp8_b M=1 decode matmul; us/call",
+        "metric": METRIC,
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -155,77 +233,81 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": fmt,
-        "data": "synthetic (seeded N(0,0.02) weights, N(0,1) x)",
+        "dtype": "+".join(fmts) + " weights x bf16 -> f32 accumulate",
+        "data": "synthetic (seeded N(0,0.02) weights, N(0,1) x, U(0.5,1.5) scales)",
         "config": {
-            "workload": desc,
-            "m": m,
-            "k": k,
-            "n": n,
-            "format": fmt,
-            "weight_bytes_per_call": wbytes,
-            "weight_copies_rotated": copies,
-            "timing": "HIP graph of the timed steps, replayed",
+            "workload": wl.desc,
+            "name": a.config,
+            "m": wl.m,
+            "k": wl.k,
+            "n": [n for n, _, _ in wl.spec],
+            "weight_bytes_per_call": wl.wbytes,
+            "weight_copies_rotated": wl.copies,
+            "timing": "HIP graph of the timed steps, replayed; events on the replay stream",
         },
-        "launch_us": {"mean": round(mean_us, 3), "median": round(med_us, 3), "min": round(durs[0], 3)},
+        "eager_us_per_call": {"median": round(eager[len(eager) // 2], 3), "min": round(eager[0], 3)},
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic_row(a.config),
+            "launch_us": round(launch_us, 3),
+            "algorithmic_bytes": wl.wbytes,
         },
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
 
 
-def cpu_baseline(linear, x, ws, scales, res, o, m, n, wbytes, seconds):
-    """The reference's CPU check path on the same inputs: x (bf16) as float32 times the held weight(s) in float32, plus
-    the config's epilogue, timed on this host's cores for about `seconds`."""
+def cpu_baseline(wl, seconds):
+    """The oracle's restatement of the reference's float32 CPU check path on the config's shapes (the held weights
+    copied from the GPU), with the config's epilogue in torch, timed on this host's cores for about `seconds`."""
     import torch
+
+    from oracle import dense_oracle as O
 
     threads = os.cpu_count()
     torch.set_num_threads(threads)
-    xc = x.reshape(m, -1).float().cpu()
-    hw = [linear.held(w).cpu().contiguous() for w in ws]
-    sc = [s.float().cpu().reshape(-1) for s in scales] if scales else None
-    rc = res.reshape(m, -1).float().cpu() if res is not None else None
+    m, o = wl.m, wl.o
+    xc = wl.x.reshape(m, -1).cpu()
+    hw = [wl.linear.held(w).cpu().contiguous() for w in wl.sets[0]]
+    sc = [s.float().cpu().reshape(-1) if s is not None else None for s in wl.scales]
+    rc = wl.res.reshape(m, -1).float().cpu() if wl.res is not None else None
 
     def step():
         if o.get("glu2"):
-            gt = (xc @ hw[0]) * sc[0]
-            up = (xc @ hw[1]) * sc[1]
-            return torch.nn.functional.silu(gt) * up
-        y = xc @ hw[0]
+            return torch.nn.functional.silu(O.ref_f32(xc, hw[0], sc[0])) * O.ref_f32(xc, hw[1], sc[1])
+        if o.get("blocks"):
+            return torch.cat([O.ref_f32(xc, h, s) for h, s in zip(hw, sc)], dim=1)
+        y = O.ref_f32(xc, hw[0], sc[0])
         if rc is not None:
             y = y + rc
         if o.get("topk"):
-            t = y.reshape(m, -1, 32)[:, : n // 32]
+            t = y.reshape(m, -1, 32)
             torch.topk(t, 8, dim=2)
             torch.topk(y, 32, dim=1)
         return y
 
-    for _ in range(3):
+    for _ in range(2):
         step()
     times = []
     t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end or len(times) < 20:
+    while time.perf_counter() < t_end or len(times) < 5:
         t0 = time.perf_counter()
         step()
         times.append(time.perf_counter() - t0)
-        if len(times) >= 2000:
-            break
     times.sort()
     med = times[len(times) // 2]
     return {
-        "value": round(wbytes / med / 1e9, 3),
+        "value": round(wl.wbytes / med / 1e9, 3),
         "unit": "GB/s",
         "us_per_call": round(med * 1e6, 1),
         "cores": threads,
         "kind": "port",
-        "sample": f"{len(times)} calls of torch float32 x @ held W on the CPU (median), the same shapes",
+        "sample": f"{len(times)} calls (median) of oracle.ref_f32 (x bf16->f32 @ held W f32) plus the epilogue, "
+        f"the full config shapes, {threads} threads, ~{seconds:.0f} s",
     }
 
 

@@ -11,7 +11,7 @@ the reference's root):
   dense_reader/linear.py:49-50); bfloat16 tiles are torch's round-to-nearest-even bf16 in face order.
 - held: the values a weight of a format holds (dense_reader/tests/test_dense_reader.py:47-49).
 - bf16_ceil, interleave_glu: dense_reader/linear.py:110-114, 122-130.
-- ref: the tests' float64 check path, test_dense_reader.py:56-58; glu_ref: test_dense_reader.py:113-115;
+- ref: the tests' float64 check path, test_dense_reader.py:56-58; ref_f32: linear.py:166-169; glu_ref: test_dense_reader.py:113-115;
   gelu_tanh in the kernels' own form, common/kernels/dense_ops.h:44-59.
 - key_bf16 / records_decode: the top-k key codec and record decode, dense_writer.cpp:215, 243-255 and
   dense_reader/linear.py:753-768; tile_topk: the records this build writes (one per 32-column tile) from an output.
@@ -294,6 +294,13 @@ def ref(x, wk, scale=None):
     """x rounded to bf16 times the held weight, float64, times the scales (test_dense_reader.py:56-58)."""
     y = x.to(torch.bfloat16).double() @ torch.as_tensor(wk).double()
     return (y * torch.as_tensor(scale).double()[None, :] if scale is not None else y).float()
+
+
+def ref_f32(x, wk, scale=None):
+    """The reference's own CPU check path, float32 (dense_reader/linear.py:166-169): x rounded to bf16, as float32,
+    times the held weight in float32, times the scales. The bench times it as the CPU baseline."""
+    y = x.to(torch.bfloat16).float() @ torch.as_tensor(wk).float()
+    return y * torch.as_tensor(scale).float()[None, :] if scale is not None else y
 
 
 def gelu_tanh(g):

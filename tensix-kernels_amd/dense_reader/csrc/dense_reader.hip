@@ -479,6 +479,19 @@ __device__ __forceinline__ void epilogue(const Args& a, const SegDev& sg, int t,
 // and runs the epilogue (so the sum order is fixed: chunks within a wavefront, wavefronts within a split, splits), then
 // resets the tile's counter for the next launch. Returns the number of partial sums now in part, 0 when this
 // workgroup is not the tile's last.
+//
+// The XCDs' L2 caches are not coherent with each other, and an agent-scope release or acquire fence writes back or
+// invalidates a whole L2 (it cost 6x the matmul itself). Instead every workspace access is a device-scope atomic
+// (relaxed): such loads and stores go to the device's point of coherence on their own. A workgroup's sums are complete
+// there before it counts itself (each thread waits for its stores, then the barrier), and the last workgroup reads
+// them only after its count has come back.
+__device__ __forceinline__ void st_dev(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int ROWS, int PW>
 __device__ __forceinline__ int gather_splits(const Args& a, int g, int split, float* part) {
     constexpr int E = PW * ROWS * 16;
@@ -488,17 +501,16 @@ __device__ __forceinline__ int gather_splits(const Args& a, int g, int split, fl
     for (int e = threadIdx.x; e < E; e += blockDim.x) {
         float v = 0.f;
         for (int w = 0; w < a.waves; ++w) v += part[w * E + e];
-        mine[e] = v;
+        st_dev(mine + e, v);
     }
-    __threadfence();
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's stores have reached the point of coherence
     __syncthreads();
     if (threadIdx.x == 0)
-        last = __hip_atomic_fetch_add(a.counters + g, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(a.splits - 1);
+        last = __hip_atomic_fetch_add(a.counters + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(a.splits - 1);
     __syncthreads();
     if (!last) return 0;
-    __threadfence();
     const float* all = a.wpart + (size_t)g * a.splits * E;
-    for (int e = threadIdx.x; e < a.splits * E; e += blockDim.x) part[e] = __builtin_nontemporal_load(all + e);
+    for (int e = threadIdx.x; e < a.splits * E; e += blockDim.x) part[e] = ld_dev(all + e);
     if (threadIdx.x == 0) __hip_atomic_store(a.counters + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     return a.splits;

@@ -16,6 +16,7 @@
  *                     kernels dense_reader.cpp, dense_compute.cpp and dense_writer.cpp
  *   dr_topk_merge  <- the host merge of top-k records, dense_reader/linear.py:747-768 (records_host) followed by a
  *                     best-k selection as lm_head_topk/lmhead.py:212-239 does on the host
+ *   dr_topk_merge_workspace_bytes <- (no counterpart: the merge runs on the host there)
  *   dr_plan        <- dense_reader/linear.py:455-495 choose/plan (the work split, for inspection only)
  *   dr_workspace_bytes <- (no counterpart: the reference's per-core accumulators live in L1 circular buffers,
  *                     linear.py:937; here a K split over workgroups meets in caller-provided device memory)
@@ -121,9 +122,12 @@ int64_t dr_workspace_bytes(const dr_launch* launch);
 int dr_matmul(const dr_launch* launch);
 
 /* The best k_out of records [n_records][2 * rows * k] (as dr_topk writes them) per row: vals [rows][k_out] fp32
- * (-inf empty), ids [rows][k_out] int32 (-1 empty), highest first, ties to the lower id. k_out <= 64. */
+ * (-inf empty), ids [rows][k_out] int32 (-1 empty), highest first, ties to the lower id. k_out <= 64. Many records
+ * are merged by several workgroups a row that meet in the workspace (dr_topk_merge_workspace_bytes; zeroed once by
+ * the caller, left with its counters at zero; merges sharing one must not overlap in time). */
+int64_t dr_topk_merge_workspace_bytes(int n_records, int rows, int k);
 int dr_topk_merge(const void* records, int n_records, int rows, int k, int fp32, int k_out, float* vals,
-                  int32_t* ids, void* stream);
+                  int32_t* ids, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* The work split for K and M: chunks (waves per output tile, each a K range of kch values) and the rows a pass
  * takes. For inspection; results depend only on what this returns. */

@@ -22,6 +22,7 @@ SYMBOLS = (
     "dr_matmul",
     "dr_workspace_bytes",
     "dr_topk_merge",
+    "dr_topk_merge_workspace_bytes",
     "dr_plan",
     "dr_status_string",
     "dr_version",
@@ -110,7 +111,10 @@ def lib():
         L.dr_workspace_bytes.restype = c_int64
         L.dr_workspace_bytes.argtypes = [ctypes.POINTER(Launch)]
         L.dr_topk_merge.restype = c_int
-        L.dr_topk_merge.argtypes = [c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p]
+        L.dr_topk_merge.argtypes = [c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_int64,
+                                    c_void_p]
+        L.dr_topk_merge_workspace_bytes.restype = c_int64
+        L.dr_topk_merge_workspace_bytes.argtypes = [c_int, c_int, c_int]
         L.dr_plan.restype = c_int
         L.dr_plan.argtypes = [c_int, c_int, ctypes.POINTER(c_int32), ctypes.POINTER(c_int32), ctypes.POINTER(c_int32)]
         L.dr_status_string.restype = ctypes.c_char_p

@@ -502,10 +502,11 @@ def matmul(
 _WORKSPACE = {}
 
 
-def _workspace(device, stream, nbytes):
-    """The split-K workspace of a device and stream: zeroed once when allocated (or grown); every launch leaves its
-    counters at zero, and launches on one stream never overlap."""
-    key = (device, stream.cuda_stream)
+def _workspace(device, stream, nbytes, kind="matmul"):
+    """The workspace of one kind of launch (the matmul's split K, or the top-k merge) on a device and stream: zeroed
+    once when allocated (or grown); every launch leaves its counters at zero, and launches on one stream never
+    overlap. The two kinds keep apart: each lays its counters out its own way."""
+    key = (device, stream.cuda_stream, kind)
     ws = _WORKSPACE.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
@@ -618,9 +619,15 @@ def topk_merge(r, rows, k, k_out=32, fp32=False, records=None):
     n = words.shape[0] if records is None else records
     vals = torch.empty(rows, k_out, dtype=torch.float32, device=r.device)
     ids = torch.empty(rows, k_out, dtype=torch.int32, device=r.device)
+    st = torch.cuda.current_stream(r.device)
+    need = _lib.lib().dr_topk_merge_workspace_bytes(n, rows, k)
+    _lib.check(_lib.DR_EINVAL if need < 0 else _lib.DR_OK, "dr_topk_merge_workspace_bytes")
+    wp, wn = None, 0
+    if need > 0:
+        ws = _workspace(r.device, st, need, "merge")
+        wp, wn = ws.data_ptr(), ws.numel()
     st = _lib.lib().dr_topk_merge(
-        words.data_ptr(), n, rows, k, int(fp32), k_out, vals.data_ptr(), ids.data_ptr(),
-        torch.cuda.current_stream(r.device).cuda_stream,
+        words.data_ptr(), n, rows, k, int(fp32), k_out, vals.data_ptr(), ids.data_ptr(), wp, wn, st.cuda_stream
     )
     _lib.check(st, "dr_topk_merge")
     return vals, ids

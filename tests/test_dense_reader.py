@@ -275,6 +275,48 @@ def test_topk_merge(device):
             same("global top-32 against torch.topk of y", vals.cpu(), torch.topk(yv, 32, dim=1).values)
 
 
+def _records(nrec, rows, k, fp32, seed, values):
+    """Synthetic top-k records [nrec, 2 * rows * k] int32: per record and row, k slots drawn from `values` (many
+    ties), some empty; ids unique."""
+    rng = np.random.default_rng(seed)
+    v = rng.choice(values, size=(nrec, rows, k)).astype(np.float32)
+    ids = (np.arange(nrec * rows * k, dtype=np.int64).reshape(nrec, rows, k) * 7919) % (1 << 30)
+    empty = rng.random((nrec, rows, k)) < 0.2
+    if fp32:
+        keys = v.view(np.uint32).astype(np.int64)
+        keys[empty] = 0xFF800000
+    else:
+        keys = O.key_bf16(O.bf16_bits(torch.from_numpy(v)))
+        keys[empty] = 0
+    ids = np.where(empty, 0xFFFFFFFF, ids)
+    words = np.concatenate([keys.reshape(nrec, rows * k), ids.reshape(nrec, rows * k)], axis=1)
+    return torch.from_numpy((words & 0xFFFFFFFF).astype(np.uint32).view(np.int32))
+
+
+@pytest.mark.parametrize("fp32", [False, True])
+def test_topk_merge_synthetic(device, fp32):
+    """dr_topk_merge against the oracle's host merge on records with heavy ties, empty slots, negative values, rows
+    with fewer valid candidates than k_out, k_out 64, and an LM-head-sized record count."""
+    ties = np.array([-3.0, -1.0, -0.5, 0.0, 0.25, 0.5, 1.0, 2.0, 2.5, 3.0], np.float32)
+    for nrec, rows, k, k_out, values in (
+        (4008, 4, 8, 32, ties),
+        (4008, 4, 8, 64, np.random.default_rng(5).standard_normal(4000).astype(np.float32)),
+        (3, 2, 4, 32, ties),  # at most 24 valid of 32 asked
+        (517, 32, 1, 16, ties),
+        (300, 3, 5, 32, ties),  # k not a multiple of 4: the element-wise loads
+        (700, 2, 16, 64, np.random.default_rng(7).standard_normal(3000).astype(np.float32)),
+        (1, 1, 32, 64, ties),
+        (16384, 1, 4, 64, np.random.default_rng(6).standard_normal(9000).astype(np.float32)),  # the most records
+    ):
+        t = _records(nrec, rows, k, fp32, nrec + rows, values)
+        hv, hi = linear.records_host(t, rows, k, fp32=fp32)
+        wv, wi = O.global_topk(hv.numpy(), hi.numpy(), k_out)
+        r = t.reshape(1, 1, nrec, -1).to(device.torch)
+        vals, ids = linear.topk_merge(r, rows, k, k_out=k_out, fp32=fp32)
+        same(f"merge values nrec {nrec} rows {rows} k {k} k_out {k_out}", vals.cpu(), torch.from_numpy(wv))
+        same(f"merge ids nrec {nrec} rows {rows} k {k} k_out {k_out}", ids.cpu().long(), torch.from_numpy(wi))
+
+
 @pytest.mark.parametrize("fmt", ["bfp8", "bfp4", "bf16"])
 def test_split_k(device, fmt):
     """A K long enough to be split over several workgroups a tile (they meet in the workspace): against the oracle,

@@ -86,7 +86,12 @@ def test_invalid_arguments_refused_on_the_host():
     L.seg[0].fmt = 7  # no such format
     assert lib.dr_matmul(ctypes.byref(L)) == _lib.DR_EINVAL
     assert lib.dr_pack(None, 0, 0, 0, 0, None, None, None, 0, 0, None) == _lib.DR_EINVAL
-    assert lib.dr_topk_merge(None, 1, 1, 1, 0, 65, None, None, None) == _lib.DR_EINVAL
+    assert lib.dr_topk_merge(None, 1, 1, 1, 0, 65, None, None, None, 0, None) == _lib.DR_EINVAL
+    assert lib.dr_topk_merge_workspace_bytes(4, 1, 8) == 0  # one workgroup a row: no workspace
+    need = lib.dr_topk_merge_workspace_bytes(4008, 4, 8)
+    assert need >= 4 * 64 * 8 * 2
+    assert lib.dr_topk_merge(8, 4008, 4, 8, 0, 32, 8, 8, None, 0, None) == _lib.DR_EINVAL  # workspace missing
+    assert lib.dr_topk_merge(8, 4008, 4, 8, 0, 32, 8, 8, 8, need - 1, None) == _lib.DR_EINVAL  # too small
     with pytest.raises(ValueError):
         _lib.check(_lib.DR_EINVAL, "x")
     with pytest.raises(RuntimeError):

@@ -183,6 +183,14 @@ def test_ref_closed_forms():
     assert abs(1.5957691216 - 2 * np.sqrt(2 / np.pi)) < 1e-10 and abs(0.0713548162 - 2 * np.sqrt(2 / np.pi) * 0.044715) < 1e-10
     assert torch.allclose(O.gelu_tanh(g), torch.nn.functional.gelu(g, approximate="tanh"), rtol=1e-7, atol=1e-12)
     assert torch.allclose(torch.nn.functional.silu(g), g / (1 + torch.exp(-g)), rtol=1e-12)
+    # ref_f32 (the reference's float32 check path): x is rounded to bf16 first (1 + 2^-9 is not a bf16), the scale
+    # multiplies columns, and on random data it stays within float32 rounding of the float64 ref
+    x = torch.tensor([[1.0 + 2.0**-9, 2.0, -3.0]])
+    s = torch.tensor([1.0, 0.5, 4.0])
+    assert torch.equal(O.ref_f32(x, w, s), torch.tensor([[2.0, 2.0, -24.0]]))
+    xr, wr = O.x_input(3, 512, 9), O.matrix(256, 512, 10).T.contiguous()
+    y64, y32 = O.ref(xr, wr).double(), O.ref_f32(xr, wr).double()
+    assert (y32 - y64).norm() / y64.norm() < 1e-6 and not torch.equal(y32, y64)
 
 
 def test_bf16_ceil_and_interleave():

@@ -397,3 +397,54 @@ def global_topk(vals, ids, k_out):
 def load_golden(path):
     with open(path) as f:
         return json.load(f)
+
+
+# --- the LM head's pick -----------------------------------------------------------------------------------------------
+
+
+def pick_token(exact, ids, vocab):
+    """The pick over rescored candidates, one row at a time (lm_head_topk/lmhead.py:40-46): the lowest id among the
+    largest values, a NaN counting as the largest; -inf marks an empty slot; vocab when nothing is there."""
+    exact = np.asarray(exact, np.float64)
+    ids = np.asarray(ids, np.int64)
+    out = np.empty(exact.shape[0], np.int64)
+    for r in range(exact.shape[0]):
+        v, i = exact[r], ids[r]
+        if np.isnan(v).any():
+            out[r] = int(i[np.isnan(v)].min())
+            continue
+        top = v.max()
+        out[r] = int(i[v == top].min()) if top > -np.inf or (v == top).any() else vocab
+    return out
+
+
+def head_logits(x, w, logits="bf16"):
+    """A bf16 host head's logits: x (bf16) times the bf16 rows w [vocab, dim] in float64, rounded to float32, then to
+    bf16 unless logits is "float32" (lm_head_topk/tests/test_lm_head.py:50-54)."""
+    z = (torch.as_tensor(x).to(torch.bfloat16).double() @ torch.as_tensor(w).to(torch.bfloat16).double().T).float()
+    return z.to(torch.bfloat16).float() if logits == "bf16" else z
+
+
+def pick_from_records(words, rows, k, top, x, w, logits="bf16", vocab=None):
+    """The device pick restated (lm_head_topk/kernels/head_pick_reader.cpp:66-90, head_pick_writer.cpp:44-66): per
+    row the best `top` valid slots by bf16 key (the earlier slot, record by record and slot by slot, first among
+    equal keys; a slot is valid when its key is not 0 and its id is below vocab), their logits from the bf16 rows
+    (head_logits), and pick_token over them. words: [records, 2 * rows * k] uint32. Returns (tokens, first
+    candidate ids, counts)."""
+    words = np.asarray(words, np.int64) & 0xFFFFFFFF
+    vocab = w.shape[0] if vocab is None else vocab
+    toks, firsts, counts = [], [], []
+    for r in range(rows):
+        keys = (words[:, r * k : (r + 1) * k] & 0xFFFF).reshape(-1)
+        ids = words[:, rows * k + r * k : rows * k + (r + 1) * k].reshape(-1)
+        order = [j for j in range(keys.size) if keys[j] != 0 and ids[j] < vocab]
+        order.sort(key=lambda j: (-int(keys[j]), j))
+        cand = [int(ids[j]) for j in order[:top]]
+        counts.append(len(cand))
+        firsts.append(cand[0] if cand else 0xFFFFFFFF)
+        if not cand:
+            toks.append(0)
+            continue
+        z = head_logits(torch.as_tensor(x)[r : r + 1], torch.as_tensor(w)[cand], logits).numpy()
+        toks.append(int(pick_token(z, np.array([cand]), vocab)[0]))
+    return np.array(toks), np.array(firsts), np.array(counts)

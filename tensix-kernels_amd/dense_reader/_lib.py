@@ -1,4 +1,4 @@
-"""ctypes binding of libdense_reader.so (the C ABI declared in include/dense_reader.h).
+"""ctypes binding of libdense_reader.so (the C ABI declared in include/dense_reader.h and include/lm_head.h).
 
 The library is built in-tree (`python -c "import __graft_entry__; __graft_entry__.build()"` at the repository root,
 or `make -C tensix-kernels_amd/dense_reader/csrc`). There is no fallback: without the library every op raises.
@@ -13,7 +13,7 @@ LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
 DR_OK, DR_EINVAL, DR_EHIP, DR_ERANGE = 0, 1, 2, 3
 
-# every symbol include/dense_reader.h declares
+# every symbol include/dense_reader.h and include/lm_head.h declare
 SYMBOLS = (
     "dr_codes_bytes",
     "dr_exps_bytes",
@@ -26,6 +26,8 @@ SYMBOLS = (
     "dr_plan",
     "dr_status_string",
     "dr_version",
+    "dr_head_pick",
+    "dr_head_pick_records",
 )
 
 c_int, c_int32, c_int64, c_void_p = ctypes.c_int, ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p
@@ -121,6 +123,11 @@ def lib():
         L.dr_status_string.argtypes = [c_int]
         L.dr_version.restype = c_int
         L.dr_version.argtypes = []
+        L.dr_head_pick.restype = c_int
+        L.dr_head_pick.argtypes = [c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_int, c_int, c_void_p, c_int64,
+                                   c_int64, c_void_p, c_void_p, c_void_p]
+        L.dr_head_pick_records.restype = c_int
+        L.dr_head_pick_records.argtypes = [c_void_p, c_int, c_int, c_int, c_int64, c_void_p, c_void_p, c_void_p, c_void_p]
         _lib = L
     return _lib
 

@@ -28,6 +28,7 @@
 #include <stdint.h>
 
 #include "dense_reader.h"
+#include "wave_select.h"
 
 // No contraction of a multiply and an add into an FMA unless the code asks for one: the compiler would otherwise
 // decide per kernel instantiation, and a weight would round differently in a block list than alone.
@@ -1007,79 +1008,7 @@ __device__ __forceinline__ unsigned long long merge_comp(uint32_t key, uint32_t 
     return ((unsigned long long)ok << 32) | (unsigned long long)(0xFFFFFFFFu - id);
 }
 
-__device__ __forceinline__ unsigned long long xor_lane(unsigned long long v, int m) {
-    const uint32_t lo = __shfl_xor((uint32_t)v, m), hi = __shfl_xor((uint32_t)(v >> 32), m);
-    return ((unsigned long long)hi << 32) | lo;
-}
-
-__device__ __forceinline__ unsigned long long from_lane(unsigned long long v, int src) {
-    const uint32_t lo = __shfl((uint32_t)v, src), hi = __shfl((uint32_t)(v >> 32), src);
-    return ((unsigned long long)hi << 32) | lo;
-}
-
-// sort the wavefront's 64 values, largest in lane 0
-__device__ __forceinline__ unsigned long long wave_sort(unsigned long long v, int lane) {
-#pragma unroll
-    for (int size = 2; size <= 64; size <<= 1) {
-#pragma unroll
-        for (int j = size >> 1; j > 0; j >>= 1) {
-            const unsigned long long p = xor_lane(v, j);
-            // blocks of `size` alternate descending / ascending (the last, 64, descending); the lower lane of a pair
-            // in a descending block keeps the larger value
-            const bool desc = (lane & size) == 0 || size == 64;
-            const bool lower = (lane & j) == 0;
-            v = (lower == desc) ? (p > v ? p : v) : (p < v ? p : v);
-        }
-    }
-    return v;
-}
-
-// list and batch sorted (largest in lane 0): the best 64 of both, sorted
-__device__ __forceinline__ unsigned long long wave_merge(unsigned long long list, unsigned long long batch, int lane) {
-    const unsigned long long r = from_lane(batch, 63 - lane);
-    unsigned long long v = list > r ? list : r;
-#pragma unroll
-    for (int j = 32; j > 0; j >>= 1) {
-        const unsigned long long p = xor_lane(v, j);
-        v = (lane & j) == 0 ? (p > v ? p : v) : (p < v ? p : v);
-    }
-    return v;
-}
-
-__device__ __forceinline__ unsigned long long lane_value(unsigned long long v, int src) {
-    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, src), hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), src);
-    return ((unsigned long long)hi << 32) | lo;
-}
-
-// A wavefront's running best: list (sorted over the lanes), thr its k_out-th value (only larger candidates can
-// enter), and up to 64 entrants waiting in pend (LDS) to be sorted and merged in at once.
-struct WaveBest {
-    unsigned long long list = 0ull, thr = 0ull;
-    int count = 0;
-
-    __device__ __forceinline__ void flush(unsigned long long* pend, int kout, int lane) {
-        if (count == 0) return;
-        __builtin_amdgcn_wave_barrier();
-        const unsigned long long v = lane < count ? pend[lane] : 0ull;
-        list = wave_merge(list, wave_sort(v, lane), lane);
-        thr = lane_value(list, kout - 1);
-        count = 0;
-        __builtin_amdgcn_wave_barrier();
-    }
-
-    // one candidate a lane (0: none)
-    __device__ __forceinline__ void add(unsigned long long v, unsigned long long* pend, int kout, int lane) {
-        unsigned long long m = __ballot(v > thr);
-        if (m == 0ull) return;
-        if (count + __popcll(m) > 64) {
-            flush(pend, kout, lane);
-            m = __ballot(v > thr);
-            if (m == 0ull) return;
-        }
-        if (v > thr) pend[count + __popcll(m & ((1ull << lane) - 1ull))] = v;
-        count += __popcll(m);
-    }
-};
+using namespace wsel;
 
 __global__ __launch_bounds__(MERGE_T) void dr_merge_k(const uint32_t* __restrict__ rec, int nrec, int rows, int k,
                                                       int fp32, int kout, int slices, int cs,

@@ -12,11 +12,11 @@ import pytest
 from dense_reader import _lib, linear
 
 ROOT = Path(__file__).resolve().parents[1]
-HEADER = ROOT / "include" / "dense_reader.h"
+HEADERS = sorted((ROOT / "include").glob("*.h"))
 
 
 def _declared():
-    text = HEADER.read_text()
+    text = "".join(h.read_text() for h in HEADERS)
     return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(dr_\w+)\s*\(", text, re.M)))
 
 
@@ -150,3 +150,50 @@ def test_interleave_and_bf16_ceil_match_oracle():
     assert torch.equal(linear.interleave_glu(g, u), O.interleave_glu(g, u))
     s = torch.rand(100, generator=torch.Generator().manual_seed(3)) + 1e-3
     assert torch.equal(linear.bf16_ceil(s), O.bf16_ceil(s))
+
+
+def test_pick_token_matches_oracle():
+    """lmhead.pick_token (host logic) against the oracle's row-by-row restatement: NaN largest, lowest id on ties,
+    -inf empty slots."""
+    import numpy as np
+    import torch
+
+    from lm_head_topk import lmhead
+    from oracle import dense_oracle as O
+
+    g = torch.Generator().manual_seed(4)
+    z = torch.randint(-3, 4, (64, 12), generator=g).float()  # many ties
+    z[z == -3] = float("-inf")
+    z[5, 3] = float("nan")
+    z[9, :] = float("-inf")
+    ids = torch.stack([torch.randperm(1000, generator=g)[:12] for _ in range(64)])
+    want = O.pick_token(z.numpy(), ids.numpy(), 1000)
+    assert np.array_equal(lmhead.pick_token(z, ids, 1000).numpy(), want)
+    assert want[5] == int(ids[5, 3])
+
+
+def test_pick_from_records_hand_case():
+    """The oracle's device-pick restatement on a hand-built record set: the best `top` by key (the earlier slot first
+    among equal keys), ids at or past vocab and empty keys skipped, then the largest logit, the lower id on a tie."""
+    import numpy as np
+    import torch
+
+    from oracle import dense_oracle as O
+
+    w = torch.zeros(8, 32)
+    w[:, 0] = torch.tensor([1.0, 5.0, 5.0, 2.0, 9.0, 3.0, 4.0, 7.0])  # logits = row 0 of w times x[0] = 1
+    x = torch.zeros(1, 32)
+    x[0, 0] = 1.0
+    key = lambda v: int(O.key_bf16(O.bf16_bits(torch.tensor([v]))[0]))  # noqa: E731
+    # one row, k 2, three records: (key, id) slots
+    rec = [[(key(5.0), 1), (key(4.0), 6)], [(key(5.0), 2), (0, 4)], [(key(9.0), 7), (key(1.0), 0)]]
+    words = np.zeros((3, 4), np.int64)
+    for p, slots in enumerate(rec):
+        for s, (kk, i) in enumerate(slots):
+            words[p, s], words[p, 2 + s] = kk, i
+    tok, first, n = O.pick_from_records(words, 1, 2, 3, x, w, "float32", vocab=8)
+    # best 3 by key: id 7 (key of 9), id 1 and id 2 (key of 5, record 0 first); logits 7, 5, 5 -> token 7
+    assert (tok[0], first[0], n[0]) == (7, 7, 3)
+    tok, first, n = O.pick_from_records(words, 1, 2, 3, x, w, "float32", vocab=7)  # id 7 past vocab
+    # best 3: ids 1, 2 (key 5), 6 (key 4); logits 5, 5, 4 -> the lower id of the tie, 1
+    assert (tok[0], first[0], n[0]) == (1, 1, 3)

@@ -63,6 +63,14 @@ CONFIGS = {
         [(128256, "bfp8", False)],
         {"topk": True},
     ),
+    "lm": (
+        "LM head to token ids, M=4 K=4096 vocab=128256 bfp8: bf16 top-8 records, the best 16 rescored from the bf16 "
+        "rows and picked on the device (lm_head_topk DeviceHead, device_pick)",
+        4,
+        4096,
+        [(128256, "bfp8", False)],
+        {"lmhead": True},
+    ),
 }
 
 
@@ -117,13 +125,32 @@ class Workload:
         fmts = {"bfp8": linear.bfloat8_b, "bfp4": linear.bfloat4_b, "bf16": linear.bfloat16}
         self.x = torch.randn(m, k, generator=g, device="cuda").to(torch.bfloat16).reshape(1, 1, m, k)
 
-        def make():
-            return [linear.native_weight(dev, torch.randn(n, k, generator=g, device="cuda") * 0.02, fmts[f])[0] for n, f, _ in ws]
+        self.heads = None
+        if o.get("lmhead"):
+            from lm_head_topk import lmhead
 
-        first = make()
+            def make():
+                w = torch.randn(ws[0][0], k, generator=g, device="cuda") * 0.02
+                h = lmhead.DeviceHead(dev, w, fmt=ws[0][1], chunks=1, k=8, top=16, device_pick=True)
+                return h
+
+            self.heads = [make()]
+        else:
+
+            def make():
+                return [
+                    linear.native_weight(dev, torch.randn(n, k, generator=g, device="cuda") * 0.02, fmts[f])[0]
+                    for n, f, _ in ws
+                ]
+
+        first = make() if self.heads is None else [self.heads[0].blocks[0][0]]
         self.wbytes = sum(w.algorithmic_bytes() for w in first)
         self.copies = max(2, math.ceil(MALL_BYTES / sum(w.nbytes() for w in first)) + 1)
-        self.sets = [first] + [make() for _ in range(self.copies - 1)]
+        if self.heads is not None:
+            self.heads += [make() for _ in range(self.copies - 1)]
+            self.sets = [[h.blocks[0][0]] for h in self.heads]
+        else:
+            self.sets = [first] + [make() for _ in range(self.copies - 1)]
         self.scales = [
             linear.scale_tensor(dev, torch.rand(n, generator=g, device="cuda") + 0.5, dtype=linear.float32) if sc else None
             for n, _, sc in ws
@@ -149,12 +176,21 @@ class Workload:
         elif o.get("topk"):
             spec = {"r": self.rec, "k": 8, "rows": self.m, "slot0": 0, "base": 0, "n": self.n, "write_y": False, "fp32": True}
             L.matmul(self.x, ws[0], None, out=self.y, topk=spec)
+        elif o.get("lmhead"):
+            h = self.heads[i % self.copies]
+            if self.m not in h.results:
+                h.logits_topk(self.x, self.m)  # (the result tensor, made once outside any graph)
+            spec = {"r": h.results[self.m], "k": h.k, "rows": self.m, "slot0": 0, "base": 0, "n": h.step, "write_y": False}
+            L.matmul(self.x, ws[0], None, out=h.y, topk=spec)
         elif self.res is not None:
             L.matmul(self.x, ws[0], None, residual=self.res, out32=True)  # (fp32 out: a fresh output each call)
         else:
             L.matmul(self.x, ws[0], None, out=self.y)
 
     def step(self, i):
+        if self.o.get("lmhead"):
+            self.heads[i % self.copies].logits_topk(self.x, self.m)
+            return
         self.kernel(i)
         if self.o.get("topk"):
             self.linear.topk_merge(self.rec, self.m, 8, k_out=32, fp32=True)
@@ -214,7 +250,7 @@ def main():
     total_ms = timed_graph(torch, wl.step, a.steps)
     ms_per_step = total_ms / a.steps
     value = wl.wbytes * a.steps / (total_ms * 1e-3) / 1e9
-    kern_ms = total_ms if not wl.o.get("topk") else timed_graph(torch, wl.kernel, a.steps)
+    kern_ms = total_ms if not (wl.o.get("topk") or wl.o.get("lmhead")) else timed_graph(torch, wl.kernel, a.steps)
     launch_us = kern_ms * 1e3 / a.steps
     achieved = wl.wbytes / (launch_us * 1e-6) / 1e9
 
@@ -284,10 +320,10 @@ def cpu_baseline(wl, seconds):
         y = O.ref_f32(xc, hw[0], sc[0])
         if rc is not None:
             y = y + rc
-        if o.get("topk"):
+        if o.get("topk") or o.get("lmhead"):
             t = y.reshape(m, -1, 32)
             torch.topk(t, 8, dim=2)
-            torch.topk(y, 32, dim=1)
+            torch.topk(y, 32 if o.get("topk") else 16, dim=1)
         return y
 
     for _ in range(2):

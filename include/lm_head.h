@@ -13,7 +13,9 @@
  *                           record by the device's own logit, through a token map)
  *
  * Both take plain device pointers and a hipStream_t (as void*), allocate nothing, and return DR_OK or a DR_E* status
- * of dense_reader.h.
+ * of dense_reader.h. Many records are selected by several workgroups a row that meet in a workspace of
+ * dr_topk_merge_workspace_bytes(n_records, rows, k) bytes (dense_reader.h; zeroed once by the caller, left with its
+ * counters at zero; launches sharing one must not overlap in time).
  */
 #ifndef LM_HEAD_H
 #define LM_HEAD_H
@@ -33,14 +35,15 @@ extern "C" {
  * candidates' count, 0 ...]. ids_out (or NULL): row 0's token also into ids_out[0]. rows <= 32; dim a multiple of 8;
  * x, head 16-byte aligned with ldx, ld_head multiples of 8. */
 int dr_head_pick(const void* records, int n_records, int rows, int k, int top, int round_bf16, const void* x, int ldx,
-                 int dim, const void* head, int64_t ld_head, int64_t vocab, void* out, void* ids_out, void* stream);
+                 int dim, const void* head, int64_t ld_head, int64_t vocab, void* out, void* ids_out, void* workspace,
+                 int64_t workspace_bytes, void* stream);
 
 /* The records' pick with no rescore: per row r < rows, the valid slot of the largest key (a NaN's key above all, -0's
  * equal to +0's), the earliest among equals; its id mapped through token_map (int32 [>= vocab], or NULL: the id).
  * out [32][32] uint32: row r = [token, the id, the valid slots' count, 0 ...] ([0, 0xFFFFFFFF, 0] when none).
  * ids_out (or NULL): row 0's token also into ids_out[0]. */
 int dr_head_pick_records(const void* records, int n_records, int rows, int k, int64_t vocab, const void* token_map,
-                         void* out, void* ids_out, void* stream);
+                         void* out, void* ids_out, void* workspace, int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

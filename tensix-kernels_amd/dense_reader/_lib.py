@@ -125,9 +125,10 @@ def lib():
         L.dr_version.argtypes = []
         L.dr_head_pick.restype = c_int
         L.dr_head_pick.argtypes = [c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_int, c_int, c_void_p, c_int64,
-                                   c_int64, c_void_p, c_void_p, c_void_p]
+                                   c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_void_p]
         L.dr_head_pick_records.restype = c_int
-        L.dr_head_pick_records.argtypes = [c_void_p, c_int, c_int, c_int, c_int64, c_void_p, c_void_p, c_void_p, c_void_p]
+        L.dr_head_pick_records.argtypes = [c_void_p, c_int, c_int, c_int, c_int64, c_void_p, c_void_p, c_void_p,
+                                           c_void_p, c_int64, c_void_p]
         _lib = L
     return _lib
 

@@ -990,134 +990,44 @@ __global__ __launch_bounds__(256) void dr_unpack_k(const uint8_t* __restrict__ c
 
 // ---- top-k merge -----------------------------------------------------------------------------------------------------
 //
-// Every candidate (a record's key and id for one row) becomes a 64-bit composite, ordered by key and then by the lower
-// id, 0 for an empty slot. The composites are distinct, so the best k_out are one set whatever order the work runs
-// in. A wavefront keeps its best 64 sorted across its lanes; a batch of 64 new candidates (one a lane) is sorted by a
-// bitonic network over the lanes and merged in (the larger of list[i] and batch[63 - i] is a bitonic sequence holding
-// the best 64 of both, which six more steps sort). The candidates of a row are cut into slices, one workgroup each
-// (the loads spread over many CUs); a workgroup merges its wavefronts' lists, and with more than one slice writes its
-// list to the workspace, where the row's last workgroup (device-scope atomics, as in the split-K sum) merges them.
+// Every slot of a row becomes a 64-bit key: the record's key (fp32 scores in key_f32's order, or the bf16 key as it
+// is) above its id complemented, 0 for an empty slot. The keys are distinct, so the best k_out are one set whatever
+// order the work runs in; wave_select.h's select_row finds them over several workgroups a row.
 
-constexpr int MERGE_T = 256;      // threads a workgroup (four wavefronts)
-constexpr int MERGE_MAXK = 64;    // k_out at most: one list is one value a lane
-constexpr int MERGE_SLICES = 64;  // workgroups a row at most
-
-__device__ __forceinline__ unsigned long long merge_comp(uint32_t key, uint32_t id, int fp32) {
-    if (id == 0xFFFFFFFFu || (!fp32 && key == 0u)) return 0ull;
-    const uint32_t ok = fp32 ? key_f32(__uint_as_float(key)) : key;
-    return ((unsigned long long)ok << 32) | (unsigned long long)(0xFFFFFFFFu - id);
-}
+constexpr int MERGE_MAXK = 64;  // k_out at most: one list is one value a lane
 
 using namespace wsel;
 
-__global__ __launch_bounds__(MERGE_T) void dr_merge_k(const uint32_t* __restrict__ rec, int nrec, int rows, int k,
-                                                      int fp32, int kout, int slices, int cs,
-                                                      unsigned long long* __restrict__ wlist,
-                                                      uint32_t* __restrict__ counters, float* __restrict__ vals,
-                                                      int32_t* __restrict__ ids) {
-    constexpr int W = MERGE_T / 64;
-    __shared__ unsigned long long lists[W][64];
-    __shared__ unsigned long long pend[W][64];
-    __shared__ int last;
-    const int r = blockIdx.x % rows, sl = blockIdx.x / rows;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const size_t rlen = 2 * (size_t)rows * k;
-    const long long total = (long long)nrec * k;
-    const long long c0 = (long long)sl * cs, c1 = min(c0 + cs, total);
-
-    // this wavefront's batches of the slice: 64 candidates each, four batches' loads in flight at a time
-    WaveBest best;
-    const int nb = (int)((c1 - c0 + 63) / 64);
-    for (int b0 = wave; b0 < nb; b0 += 4 * W) {
-        unsigned long long v[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const long long c = c0 + (long long)(b0 + u * W) * 64 + lane;
-            const long long cc = c < c1 ? c : c0;  // (in bounds; masked below)
-            const long long ri = cc / k;
-            const int j = (int)(cc - ri * k);
-            const uint32_t* kp = rec + (size_t)ri * rlen + (size_t)r * k + j;
-            const uint32_t key = kp[0], id = kp[(size_t)rows * k];
-            v[u] = c < c1 ? merge_comp(key, id, fp32) : 0ull;
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) best.add(v[u], pend[wave], kout, lane);
-    }
-    best.flush(pend[wave], kout, lane);
-    // the workgroup's list: wavefront 0 merges the others'
-    lists[wave][lane] = best.list;
-    __syncthreads();
-    unsigned long long list = best.list;
-    if (wave == 0) {
-#pragma unroll
-        for (int w = 1; w < W; ++w) list = wave_merge(list, lists[w][lane], lane);
-    }
-    if (slices > 1) {
-        // meet the row's other workgroups in the workspace; the last one merges every slice's list
-        if (wave == 0) {
-            __hip_atomic_store(wlist + ((size_t)r * slices + sl) * 64 + lane, list, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-            __builtin_amdgcn_s_waitcnt(0);
-        }
-        __syncthreads();
-        if (threadIdx.x == 0)
-            last = __hip_atomic_fetch_add(counters + r, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                   (uint32_t)(slices - 1);
-        __syncthreads();
-        if (!last) return;
-        // every list of this wavefront's share loaded at once (slices <= MERGE_SLICES), then added in turn
-        constexpr int Q = MERGE_SLICES / W;
-        unsigned long long lv[Q];
-#pragma unroll
-        for (int i = 0; i < Q; ++i) {
-            const int q = min(wave + i * W, slices - 1);
-            lv[i] = __hip_atomic_load(wlist + ((size_t)r * slices + q) * 64 + lane, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT);
-        }
-        // (each list is sorted already: a bitonic merge takes it in)
-        unsigned long long mine = 0ull;
-#pragma unroll
-        for (int i = 0; i < Q; ++i)
-            if (wave + i * W < slices) mine = wave_merge(mine, lv[i], lane);  // (uniform)
-        lists[wave][lane] = mine;
-        __syncthreads();
-        if (wave == 0) {
-            list = mine;
-#pragma unroll
-            for (int w = 1; w < W; ++w) list = wave_merge(list, lists[w][lane], lane);
-            if (lane == 0) __hip_atomic_store(counters + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__global__ __launch_bounds__(SEL_T) void dr_merge_k(SelArgs A, int fp32, float* __restrict__ vals,
+                                                    int32_t* __restrict__ ids) {
+    __shared__ SelShared sh;
+    const int r = blockIdx.x % A.rows, sl = blockIdx.x / A.rows;
+    const int lane = threadIdx.x & 63;
+    unsigned long long list;
+    int count;
+    const bool mine = select_row(
+        A, r, sl,
+        [fp32](uint32_t key, uint32_t id, uint32_t) -> unsigned long long {
+            if (id == 0xFFFFFFFFu || (!fp32 && key == 0u)) return 0ull;
+            const uint32_t ok = fp32 ? key_f32(__uint_as_float(key)) : key;
+            return ((unsigned long long)ok << 32) | (unsigned long long)(0xFFFFFFFFu - id);
+        },
+        sh, list, count);
+    if (!mine || threadIdx.x >= 64 || lane >= A.keep) return;
+    float val = -__builtin_huge_valf();
+    int32_t id = -1;
+    if (list != 0ull) {
+        const uint32_t ok = (uint32_t)(list >> 32);
+        id = (int32_t)(0xFFFFFFFFu - (uint32_t)(list & 0xFFFFFFFFu));
+        if (fp32) {
+            val = __uint_as_float((ok >> 31) ? (ok ^ 0x80000000u) : ~ok);
+        } else {
+            const uint32_t bits = ok >= 0x8000u ? (ok & 0x7FFFu) : (~ok & 0xFFFFu);
+            val = __uint_as_float(bits << 16);
         }
     }
-    if (wave == 0 && lane < kout) {
-        float val = -__builtin_huge_valf();
-        int32_t id = -1;
-        if (list != 0ull) {
-            const uint32_t ok = (uint32_t)(list >> 32);
-            id = (int32_t)(0xFFFFFFFFu - (uint32_t)(list & 0xFFFFFFFFu));
-            if (fp32) {
-                val = __uint_as_float((ok >> 31) ? (ok ^ 0x80000000u) : ~ok);
-            } else {
-                const uint32_t bits = ok >= 0x8000u ? (ok & 0x7FFFu) : (~ok & 0xFFFFu);
-                val = __uint_as_float(bits << 16);
-            }
-        }
-        vals[(size_t)r * kout + lane] = val;
-        ids[(size_t)r * kout + lane] = id;
-    }
-}
-
-// the workspace of a merge: a counter a row (256-byte aligned block), then each row's slice lists [slices][64]
-inline int64_t merge_counter_bytes(int rows) { return ((int64_t)rows * 4 + 255) / 256 * 256; }
-
-// the merge's slices a row: about 1024 candidates each (four batches of 64 a wavefront), at most MERGE_SLICES
-void merge_plan(int n_records, int k, int* slices, int* cs) {
-    const long long total = (long long)n_records * k;
-    int sl = (int)std::min<long long>(MERGE_SLICES, std::max<long long>(1, (total + 1023) / 1024));
-    long long c = (total + sl - 1) / sl;
-    c = (c + 63) / 64 * 64;
-    sl = (int)((total + c - 1) / c);
-    *slices = sl;
-    *cs = (int)c;
+    vals[(size_t)r * A.keep + lane] = val;
+    ids[(size_t)r * A.keep + lane] = id;
 }
 
 inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
@@ -1378,10 +1288,7 @@ int dr_matmul(const dr_launch* L) {
 
 int64_t dr_topk_merge_workspace_bytes(int n_records, int rows, int k) {
     if (n_records < 1 || rows < 1 || k < 1) return -1;
-    int slices, cs;
-    merge_plan(n_records, k, &slices, &cs);
-    if (slices == 1) return 0;
-    return merge_counter_bytes(rows) + (int64_t)rows * slices * 64 * 8;
+    return select_workspace_bytes(n_records, rows, k);
 }
 
 int dr_topk_merge(const void* records, int n_records, int rows, int k, int fp32, int k_out, float* vals,
@@ -1390,17 +1297,16 @@ int dr_topk_merge(const void* records, int n_records, int rows, int k, int fp32,
         k_out > MERGE_MAXK)
         return DR_EINVAL;
     if ((int64_t)n_records * k > ((int64_t)1 << 40)) return DR_ERANGE;
-    int slices, cs;
-    merge_plan(n_records, k, &slices, &cs);
-    const int64_t need = dr_topk_merge_workspace_bytes(n_records, rows, k);
-    if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return DR_EINVAL;
-    uint32_t* counters = reinterpret_cast<uint32_t*>(workspace);
-    unsigned long long* wlist =
-        need > 0 ? reinterpret_cast<unsigned long long*>(reinterpret_cast<uint8_t*>(workspace) + merge_counter_bytes(rows))
-                 : nullptr;
-    hipLaunchKernelGGL(dr_merge_k, dim3(rows * slices), dim3(MERGE_T), 0, S(stream),
-                       reinterpret_cast<const uint32_t*>(records), n_records, rows, k, fp32, k_out, slices, cs, wlist,
-                       counters, vals, ids);
+    SelArgs A{reinterpret_cast<const uint32_t*>(records), n_records, rows, k, k_out, 1, 0, nullptr, nullptr};
+    select_plan(n_records, k, &A.slices, &A.cs);
+    const int64_t need = select_workspace_bytes(n_records, rows, k);
+    if (need > 0) {
+        if (workspace == nullptr || workspace_bytes < need) return DR_EINVAL;
+        A.counters = reinterpret_cast<uint32_t*>(workspace);
+        A.wlist = reinterpret_cast<unsigned long long*>(reinterpret_cast<uint8_t*>(workspace) +
+                                                        select_counter_bytes(rows));
+    }
+    hipLaunchKernelGGL(dr_merge_k, dim3(rows * A.slices), dim3(SEL_T), 0, S(stream), A, fp32, vals, ids);
     return hip_status(hipGetLastError());
 }
 

@@ -5,7 +5,8 @@ lmhead.DeviceHead's device part leaves, per row, the best candidates of every 32
 top-k result tensor (linear.matmul's topk records). pick() takes the best `top` of them by the device's logit,
 recomputes their logits from the bf16 head rows (bf16 x times bf16 rows, summed in float32, rounded to bf16 unless
 logits="float32") and picks the largest (the lowest id on ties, a NaN counting as the largest: lmhead.pick_token's
-rule), one workgroup a row, in one launch with no host reads (graph-capturable):
+rule), in one launch with no host reads (graph-capturable; several workgroups a row meet in the top-k merge's
+workspace):
 
   rows = head_rows(device, weight)                    # the bf16 head [vocab, dim] on the device, one row a token
   out = pick(records, x, rows, nrows, k, top=16)      # [1, 1, 32, 32] int32; row r: token, device best, count
@@ -25,7 +26,7 @@ import torch
 
 sys.path.insert(0, str(Path(__file__).resolve().parents[1]))
 from common import device as dev  # noqa: E402
-from dense_reader import _lib  # noqa: E402
+from dense_reader import _lib, linear  # noqa: E402
 
 TILE = 32
 
@@ -63,6 +64,16 @@ def _out_page(device):
     return torch.zeros(1, 1, TILE, TILE, dtype=torch.int32, device=device)
 
 
+def _select_workspace(device, stream, n_records, rows, k):
+    """(pointer, bytes) of the selection's workspace (the top-k merge's), or (None, 0) when one workgroup a row does."""
+    need = _lib.lib().dr_topk_merge_workspace_bytes(n_records, rows, k)
+    _lib.check(_lib.DR_EINVAL if need < 0 else _lib.DR_OK, "dr_topk_merge_workspace_bytes")
+    if need == 0:
+        return None, 0
+    ws = linear._workspace(device, stream, need, "merge")
+    return ws.data_ptr(), ws.numel()
+
+
 def _words(records, nrows, k):
     w = records.reshape(records.shape[-2], -1)
     if w.dtype == torch.bfloat16:
@@ -95,10 +106,12 @@ def pick(records, x, rows_t, nrows, k, top=16, logits="bf16", out=None, valid=No
     assert out.dtype == torch.int32 and out.numel() >= TILE * TILE and out.is_contiguous(), (out.shape, out.dtype)
     if ids_out is not None:
         check_ids_out(ids_out)
+    stream = torch.cuda.current_stream(x.device)
+    wp, wn = _select_workspace(x.device, stream, words.shape[0], nrows, k)
     st = _lib.lib().dr_head_pick(
         words.data_ptr(), words.shape[0], nrows, k, top, int(logits == "bf16"), x2.data_ptr(), x2.shape[1], dim,
-        rows_t.data_ptr(), dim, vocab, out.data_ptr(), None if ids_out is None else ids_out.data_ptr(),
-        torch.cuda.current_stream(x.device).cuda_stream,
+        rows_t.data_ptr(), dim, vocab, out.data_ptr(), None if ids_out is None else ids_out.data_ptr(), wp, wn,
+        stream.cuda_stream,
     )
     _lib.check(st, "dr_head_pick")
     return out
@@ -136,9 +149,11 @@ def pick_records(records, nrows, k, vocab, tmap=None, out=None, ids_out=None):
         out = _out_page(records.device)
     if ids_out is not None:
         check_ids_out(ids_out)
+    stream = torch.cuda.current_stream(records.device)
+    wp, wn = _select_workspace(records.device, stream, words.shape[0], nrows, k)
     st = _lib.lib().dr_head_pick_records(
         words.data_ptr(), words.shape[0], nrows, k, vocab, None if tmap is None else tmap.data_ptr(), out.data_ptr(),
-        None if ids_out is None else ids_out.data_ptr(), torch.cuda.current_stream(records.device).cuda_stream,
+        None if ids_out is None else ids_out.data_ptr(), wp, wn, stream.cuda_stream,
     )
     _lib.check(st, "dr_head_pick_records")
     return out

@@ -339,3 +339,27 @@ def test_split_k(device, fmt):
             same(f"{fmt} K {k} rows {m} block list (split K)", host(one, m, 12 * 32 + 256)[:, :n],
                  host(two, m, 12 * 32 + 256)[:, :n])
             same(f"{fmt} K {k} rows {m} block list second block", host(one, m, 640)[:, 384:], host(two, m, 640)[:, 384:])
+
+
+def test_pack_cache(device, tmp_path):
+    """native_weight_cached: the first call packs and writes the cache, the second reads it back; the weights are
+    byte for byte the same and the matmul bit for bit; another weight's call is refused until rebuild."""
+    from dense_reader import pack_cache as pc
+
+    k, n = 512, 320
+    for fmt, cs in (("bfp8", False), ("bfp4", True), ("bf16", False)):
+        wt = matrix(n, k, 80)
+        path = tmp_path / f"w_{fmt}"
+        w1, s1 = pc.native_weight_cached(device, wt, DTYPES[fmt], path, col_scale=cs)
+        w2, s2 = pc.native_weight_cached(device, wt, DTYPES[fmt], path, col_scale=cs)
+        same(f"pack cache {fmt}: codes", w2.codes.cpu(), w1.codes.cpu())
+        if w1.exps is not None:
+            same(f"pack cache {fmt}: exponents", w2.exps.cpu(), w1.exps.cpu())
+        same(f"pack cache {fmt}: scales", s2.cpu(), s1.cpu())
+        x, tx = x_input(device, 2, k, 81)
+        same(f"pack cache {fmt}: matmul", linear.matmul(tx, w2, s2).cpu(), linear.matmul(tx, w1, s1).cpu())
+        with pytest.raises(pc.PackCacheMismatch):
+            pc.native_weight_cached(device, matrix(n, k, 82), DTYPES[fmt], path, col_scale=cs)
+        w3, _ = pc.native_weight_cached(device, matrix(n, k, 82), DTYPES[fmt], path, col_scale=cs, rebuild=True)
+        w4, _ = pc.native_weight_cached(device, matrix(n, k, 82), DTYPES[fmt], path, col_scale=cs)
+        same(f"pack cache {fmt}: rebuilt", w4.codes.cpu(), w3.codes.cpu())

@@ -8,6 +8,7 @@ import subprocess
 from pathlib import Path
 
 import pytest
+import torch
 
 from dense_reader import _lib, linear
 
@@ -197,3 +198,33 @@ def test_pick_from_records_hand_case():
     tok, first, n = O.pick_from_records(words, 1, 2, 3, x, w, "float32", vocab=7)  # id 7 past vocab
     # best 3: ids 1, 2 (key 5), 6 (key 4); logits 5, 5, 4 -> the lower id of the tie, 1
     assert (tok[0], first[0], n[0]) == (1, 1, 3)
+
+
+def test_pack_cache_files(tmp_path):
+    """The pack cache's file logic, with arrays of a made-up pack (no GPU): written whole then taken; a different
+    meta refused and left as it is; a damaged array refused; rebuild hands the call back to be packed again."""
+    import json
+
+    import numpy as np
+
+    from dense_reader import pack_cache as pc
+
+    path = tmp_path / "w"
+    meta = {"version": pc.PACK_VERSION, "format": "bfloat8_b", "k": 64, "n": 32, "weight": "x"}
+    arrays = {"codes": np.arange(256, dtype=np.uint8), "scale": np.ones(32, np.float32)}
+    assert pc.cache_read(path, meta) is None  # none yet
+    pc.cache_write(path, meta, arrays)
+    assert not (tmp_path / "w.tmp").exists()
+    got = pc.cache_read(path, meta)
+    assert set(got) == {"codes", "scale"} and np.array_equal(got["codes"], arrays["codes"])
+    other = dict(meta, weight="y")
+    with pytest.raises(pc.PackCacheMismatch, match="weight"):
+        pc.cache_read(path, other)
+    assert json.loads((path / "meta.json").read_text()) == meta  # not overwritten
+    assert pc.cache_read(path, other, rebuild=True) is None
+    np.save(path / "codes.npy", np.zeros(256, np.uint8))  # damaged
+    with pytest.raises(pc.PackCacheMismatch, match="damaged"):
+        pc.cache_read(path, meta)
+    assert pc.cache_read(path, meta, verify=False) is not None
+    a = torch.arange(10000, dtype=torch.float32).reshape(100, 100)
+    assert pc.fingerprint(a) == pc.fingerprint(a.clone()) and pc.fingerprint(a) != pc.fingerprint(a + 1)

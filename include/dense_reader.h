@@ -18,6 +18,8 @@
  *                     best-k selection as lm_head_topk/lmhead.py:212-239 does on the host
  *   dr_topk_merge_workspace_bytes <- (no counterpart: the merge runs on the host there)
  *   dr_plan        <- dense_reader/linear.py:455-495 choose/plan (the work split, for inspection only)
+ *   dr_pack_int4, dr_int4_scales_bytes, dr_pack_int4_scales <- int4/w4a16.py:69-97 int4_weight / group_scales
+ *                     (the int4 weight's conversions; dr_matmul with a DR_INT4 segment replaces w4a16_linear)
  *   dr_workspace_bytes <- (no counterpart: the reference's per-core accumulators live in L1 circular buffers,
  *                     linear.py:937; here a K split over workgroups meets in caller-provided device memory)
  */
@@ -30,10 +32,12 @@
 extern "C" {
 #endif
 
-/* weight formats (the reference's ttnn.bfloat8_b, ttnn.bfloat4_b, ttnn.bfloat16) */
+/* weight formats (the reference's ttnn.bfloat8_b, ttnn.bfloat4_b, ttnn.bfloat16; DR_INT4 the W4A16 weight of
+ * int4/w4a16.py: codes q in -7..7 with one bf16 scale per output column and 32 inputs, the weight q * s) */
 #define DR_BFP8 0
 #define DR_BFP4 1
 #define DR_BF16 2
+#define DR_INT4 3
 
 /* statuses */
 #define DR_OK 0
@@ -57,6 +61,17 @@ int64_t dr_exps_bytes(int fmt, int k_pad, int n_pad);
 int dr_pack(const float* w, int64_t ld_w, int n, int k, int fmt, const float* col_div, void* codes, void* exps,
             int n_pad, int k_pad, void* stream);
 
+/* Pack int4 codes q [N][ld_q] int8 (-7..7; device) as a DR_INT4 weight [K, N]: bfloat4_b's code layout (nibbles
+ * u = q + 8), no exponents; zeros past N and K up to n_pad, k_pad (replaces int4/w4a16.py:69-86 int4_weight's
+ * conversion). */
+int dr_pack_int4(const int8_t* q, int64_t ld_q, int n, int k, void* codes, int n_pad, int k_pad, void* stream);
+
+/* Lay out the group scales s [N][ld_s] bf16 (one per output column and 32 inputs; device) for a DR_INT4 weight:
+ * out [n_pad / 16][k_pad / 128][4][16] bf16, zeros past N and K (dr_int4_scales_bytes; replaces int4/w4a16.py:89-97
+ * group_scales). */
+int64_t dr_int4_scales_bytes(int k_pad, int n_pad);
+int dr_pack_int4_scales(const uint16_t* s, int64_t ld_s, int n, int k, void* out, int n_pad, int k_pad, void* stream);
+
 /* The held values of a packed weight: out [K][ld_out] fp32 (device), columns 0 .. n-1. */
 int dr_unpack(const void* codes, const void* exps, int fmt, int n, int k, int n_pad, int k_pad, float* out,
               int64_t ld_out, void* stream);
@@ -72,7 +87,8 @@ typedef struct dr_segment {
     const void* exps;
     const void* codes_up;
     const void* exps_up;
-    const void* scale;    /* per weight column scales [n] or NULL (unit) */
+    const void* scale;    /* per weight column scales [n] or NULL (unit); DR_INT4: its group scales
+                             (dr_pack_int4_scales), required */
     const void* scale_up; /* glu 2: the up weight's scales or NULL */
     int32_t scale_f32;    /* scales are fp32 (1) or bf16 (0) */
     int32_t col0;         /* first output column in y, a multiple of 32 */
@@ -118,7 +134,8 @@ typedef struct dr_launch {
  * Launches that share one workspace must not overlap in time (one stream). */
 int64_t dr_workspace_bytes(const dr_launch* launch);
 
-/* y = the launch's fused matmul. Allocates nothing. */
+/* y = the launch's fused matmul. Allocates nothing. A DR_INT4 weight goes alone (one segment, no GLU, residual or
+ * top-k) and takes its rows two at a time (int4/w4a16.py:170-253 w4a16_linear takes one token). */
 int dr_matmul(const dr_launch* launch);
 
 /* The best k_out of records [n_records][2 * rows * k] (as dr_topk writes them) per row: vals [rows][k_out] fp32

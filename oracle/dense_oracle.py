@@ -448,3 +448,58 @@ def pick_from_records(words, rows, k, top, x, w, logits="bf16", vocab=None):
         z = head_logits(torch.as_tensor(x)[r : r + 1], torch.as_tensor(w)[cand], logits).numpy()
         toks.append(int(pick_token(z, np.array([cand]), vocab)[0]))
     return np.array(toks), np.array(firsts), np.array(counts)
+
+
+# --- int4 W4A16 -------------------------------------------------------------------------------------------------------
+
+
+def int4_dequantized(codes, scales):
+    """The float [N_out, K] weight q * s with s rounded to bf16 (int4/w4a16.py:100-102)."""
+    codes = torch.as_tensor(codes)
+    s = torch.as_tensor(scales).to(torch.bfloat16).double()
+    return codes.double() * s.repeat_interleave(32, dim=1)
+
+
+def int4_ref(x, codes, scales):
+    """x rounded to bf16 times (q * s).T in float64 (int4/w4a16.py:105-107, in float64 here)."""
+    return (torch.as_tensor(x).to(torch.bfloat16).double() @ int4_dequantized(codes, scales).T).float()
+
+
+def int4_nibbles(codes):
+    """The reference's int4 tile bytes of codes [K, N] (int4/w4a16.py:59-66), one value at a time: tile (kt, nt), face
+    f = 2 (r // 16) + c // 16 of element (r, c), position 256 f + 16 (r % 16) + c % 16 in the tile, value sign << 3 |
+    |q|, element 2i in the low nibble of byte i."""
+    codes = np.asarray(codes, np.int64)
+    k, n = codes.shape
+    out = np.zeros((k // 32, n // 32, 512), np.uint8)
+    for kk in range(k):
+        for nn in range(n):
+            q = int(codes[kk, nn])
+            v = (8 if q < 0 else 0) | abs(q)
+            r, c = kk % 32, nn % 32
+            pos = 256 * (2 * (r // 16) + c // 16) + 16 * (r % 16) + c % 16
+            out[kk // 32, nn // 32, pos // 2] |= v << (4 * (pos % 2))
+    return out
+
+
+def int4_layout(codes, n_pad, k_pad):
+    """codes [N, K] (-7..7) in this build's int4 layout: bfloat4_b's codes (panel of 16 columns, k-block of 128, lane
+    16 kq + c its 16 bytes, dword d holding k 8 d + j in the low nibble of byte j and 8 d + 4 + j in the high one, each
+    u = q + 8); zeros (u = 8) past N and K. Returns uint8 [n_pad * k_pad / 2]."""
+    codes = np.asarray(codes, np.int64)
+    n, k = codes.shape
+    q = np.zeros((n_pad, k_pad), np.int64)
+    q[:n, :k] = codes
+    u = (q + 8).reshape(n_pad // 16, 16, k_pad // 128, 4, 4, 2, 4)  # panel, c, block, kq, d, h, j
+    u = u.transpose(0, 2, 3, 1, 4, 6, 5)  # panel, block, kq, c, d, j, h
+    return (u[..., 0] | (u[..., 1] << 4)).astype(np.uint8).reshape(-1)
+
+
+def int4_scales_layout(scales, n_pad, k_pad):
+    """Group scales [N, K / 32] (bf16 bits as uint16) in this build's order [panel, k-block, kq, c]; zeros past N and
+    K. Returns uint16 [n_pad / 16 * k_pad / 128 * 64]."""
+    s = np.asarray(scales, np.uint16)
+    n, g = s.shape
+    full = np.zeros((n_pad, k_pad // 32), np.uint16)
+    full[:n, :g] = s
+    return full.reshape(n_pad // 16, 16, k_pad // 128, 4).transpose(0, 2, 3, 1).reshape(-1)

@@ -18,6 +18,9 @@ SYMBOLS = (
     "dr_codes_bytes",
     "dr_exps_bytes",
     "dr_pack",
+    "dr_pack_int4",
+    "dr_int4_scales_bytes",
+    "dr_pack_int4_scales",
     "dr_unpack",
     "dr_matmul",
     "dr_workspace_bytes",
@@ -106,6 +109,12 @@ def lib():
         L.dr_exps_bytes.argtypes = [c_int, c_int, c_int]
         L.dr_pack.restype = c_int
         L.dr_pack.argtypes = [c_void_p, c_int64, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p]
+        L.dr_pack_int4.restype = c_int
+        L.dr_pack_int4.argtypes = [c_void_p, c_int64, c_int, c_int, c_void_p, c_int, c_int, c_void_p]
+        L.dr_int4_scales_bytes.restype = c_int64
+        L.dr_int4_scales_bytes.argtypes = [c_int, c_int]
+        L.dr_pack_int4_scales.restype = c_int
+        L.dr_pack_int4_scales.argtypes = [c_void_p, c_int64, c_int, c_int, c_void_p, c_int, c_int, c_void_p]
         L.dr_unpack.restype = c_int
         L.dr_unpack.argtypes = [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_int64, c_void_p]
         L.dr_matmul.restype = c_int

@@ -40,7 +40,9 @@ constexpr int KALIGN = 256;  // K padding: one exponent group; a multiple of eve
 constexpr int MAXW = 8;      // wavefronts a workgroup at most (512 threads: up to 256 VGPRs a lane)
 constexpr int TILE = 32;
 
-__host__ __device__ constexpr int kblk(int fmt) { return fmt == DR_BFP8 ? 64 : (fmt == DR_BFP4 ? 128 : 32); }
+__host__ __device__ constexpr int kblk(int fmt) {
+    return fmt == DR_BFP8 ? 64 : (fmt == DR_BFP4 || fmt == DR_INT4) ? 128 : 32;
+}
 
 // the byte of a panel's exponents that holds k (see the layout above)
 __host__ __device__ constexpr int exp_off(int fmt, int k) {
@@ -72,6 +74,7 @@ struct SegDev {
     const uint8_t* exps_up;
     const void* scale;
     const void* scale_up;
+    const uint16_t* gscale;  // DR_INT4: the group scales [panel][k-block][4][16] bf16
     int fmt, n, n_pad, glu, scale_f32, col0;
     int n_out, tiles, tile_begin;
     unsigned pstride;  // bytes of codes a panel
@@ -114,11 +117,20 @@ __device__ __forceinline__ void fmac_bcast(float& acc, float s, float f) {
                      : "+v"(acc) : "v"(s), "v"(f), "i"(I));
 }
 
-// acc += dot(broadcast(bf16 pair p from lane J of this row of 16), bf16 pair a), one VOP2 with DPP (same hazard rule)
-template <int J, bool NOP>
+// acc += dot(broadcast(bf16 pair p from lane J of this row of 16), bf16 pair a), one VOP2 with DPP (same hazard rule
+// for p). A DOT's result must be 3 wait states before any other VALU instruction reads it (another v_dot2c reading it
+// as its accumulator needs none); the compiler sees no DOT in inline asm, so the last dot2c into an accumulator before
+// other code reads it carries an s_nop 2 (LAST = true).
+template <int J, bool NOP, bool LAST = false>
 __device__ __forceinline__ void dot2_bcast(float& acc, uint32_t p, uint32_t a) {
-    if constexpr (NOP)
+    if constexpr (NOP && LAST)
+        asm volatile("s_nop 1\n\tv_dot2c_f32_bf16_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf\n\ts_nop 2"
+                     : "+v"(acc) : "v"(p), "v"(a), "i"(J));
+    else if constexpr (NOP)
         asm volatile("s_nop 1\n\tv_dot2c_f32_bf16_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+                     : "+v"(acc) : "v"(p), "v"(a), "i"(J));
+    else if constexpr (LAST)
+        asm volatile("v_dot2c_f32_bf16_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf\n\ts_nop 2"
                      : "+v"(acc) : "v"(p), "v"(a), "i"(J));
     else
         asm volatile("v_dot2c_f32_bf16_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
@@ -216,7 +228,11 @@ __device__ __forceinline__ void bfp4_step(float (&acc)[PW][MR], const uint32_t (
             dot2_bcast<4 * D + 0, D == 0>(acc[q][m], xs[q][m], a0);
             dot2_bcast<4 * D + 1, false>(acc[q][m], xs[q][m], a1);
             dot2_bcast<4 * D + 2, false>(acc[q][m], xs[q][m], a2);
-            dot2_bcast<4 * D + 3, false>(acc[q][m], xs[q][m], a3);
+            // (every other accumulator has at least 4 more dot2c after its last one)
+            if (D == 3 && q == PW - 1 && m == MR - 1)
+                dot2_bcast<4 * D + 3, false, true>(acc[q][m], xs[q][m], a3);
+            else
+                dot2_bcast<4 * D + 3, false>(acc[q][m], xs[q][m], a3);
         }
     }
     if constexpr (D + 1 < 4) bfp4_step<D + 1, MR, PW>(acc, xs, c);
@@ -278,6 +294,71 @@ __device__ __forceinline__ void chunk_bfp4(const Args& a, const uint8_t* const* 
             }
         }
         bfp4_step<0, MR, PW>(acc, xs, c[u].c);
+    }
+}
+
+// int4 (W4A16): the bfloat4_b code layout with no exponents (every value q = u - 8) and a bf16 scale per column and 32
+// k (int4/w4a16.py:1-19). Lane (kq, c)'s 32 k of a block are one scale group, so the lane's block sum is a group sum:
+// bf16 dot2 of x pairs (as they are) against 136 + q, less 136 times the row's x sum, times the lane's scale. Loads as
+// chunk_bfp4: x first, then the scales, then the codes.
+template <int MR, int PW>
+__device__ __forceinline__ void chunk_int4(const Args& a, const uint8_t* const* cb, const uint16_t* const* gs, int k0,
+                                           int k1, int lane, float (&acc)[PW][MR]) {
+    const int kq = lane >> 4, i = lane & 15;
+    const int g0 = k0 >> 8;
+    const bool two = k1 - k0 > 256;
+    const int g1 = two ? g0 + 1 : g0;
+    uint32_t xp[4][MR];
+    uint32_t sc[4][PW];
+    Codes<PW> c[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int b = 2 * (u < 2 ? g0 : g1) + (u & 1);
+        const int kp = b * 128 + kq * 32 + 2 * i;
+        const int kc = min(kp, a.k - 2);
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            const int mc = min(m, a.m - 1);
+            const uint32_t v = *reinterpret_cast<const uint32_t*>(a.x + (size_t)mc * a.ldx + kc);
+            xp[u][m] = v & opaque((kp < a.k && m < a.m) ? 0xFFFFFFFFu : 0u);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int b = 2 * (u < 2 ? g0 : g1) + (u & 1);
+#pragma unroll
+        for (int q = 0; q < PW; ++q) sc[u][q] = gs[q][(size_t)b * 64 + lane];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int b = 2 * (u < 2 ? g0 : g1) + (u & 1);
+#pragma unroll
+        for (int q = 0; q < PW; ++q) c[u].c[q] = *reinterpret_cast<const uint4*>(cb[q] + (uint32_t)(b * 1024 + lane * 16));
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        if (u == 2 && !two) break;
+        uint32_t xs[PW][MR];
+        float rs[MR];  // the row's x sum (the 16 lanes' pairs): 136 times it is in every dot of the row
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            float v = bf16_to_f32(xp[u][m] & 0xFFFFu) + bf16_to_f32(xp[u][m] >> 16);
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o);
+            rs[m] = 136.f * v;
+#pragma unroll
+            for (int q = 0; q < PW; ++q) xs[q][m] = xp[u][m];
+        }
+        float t[PW][MR];
+#pragma unroll
+        for (int q = 0; q < PW; ++q)
+#pragma unroll
+            for (int m = 0; m < MR; ++m) t[q][m] = 0.f;
+        bfp4_step<0, MR, PW>(t, xs, c[u].c);
+#pragma unroll
+        for (int q = 0; q < PW; ++q)
+#pragma unroll
+            for (int m = 0; m < MR; ++m) acc[q][m] = __builtin_fmaf(t[q][m] - rs[m], bf16_to_f32(sc[u][q]), acc[q][m]);
     }
 }
 
@@ -555,6 +636,11 @@ __global__ __launch_bounds__(512) void dr_gemv(const Args a) {
         const int k0 = ch * a.kch, k1 = min(k0 + a.kch, a.k_pad);
         if (fmt == DR_BFP8) {
             chunk_bfp8<MR, PW>(a, cb, eb, k0, k1, lane, acc);
+        } else if (FMT == DR_INT4) {
+            const uint16_t* gs[PW];
+#pragma unroll
+            for (int q = 0; q < PW; ++q) gs[q] = sg.gscale + (size_t)(2 * t + q) * (a.k_pad / 128) * 64;
+            chunk_int4<MR, PW>(a, cb, gs, k0, k1, lane, acc);
         } else if (fmt == DR_BFP4) {
             float sx[PW][MR];
 #pragma unroll
@@ -988,6 +1074,43 @@ __global__ __launch_bounds__(256) void dr_unpack_k(const uint8_t* __restrict__ c
     out[(long long)kk * ld_out + col] = val;
 }
 
+// int4 codes q [n][ldq] (-7..7) to the bfloat4_b code layout (u = q + 8): one thread per (panel, k-block, lane), the
+// lane's 16 bytes (dword d: k 8 d + j low, 8 d + 4 + j high, of its 32 k)
+__global__ __launch_bounds__(256) void dr_pack_int4_k(const int8_t* __restrict__ q, long long ldq, int n, int k,
+                                                      uint8_t* __restrict__ codes, int n_pad, int k_pad) {
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const int nblk = k_pad / 128;
+    if (idx >= (long long)(n_pad / 16) * nblk * 64) return;
+    const int lane = (int)(idx & 63), b = (int)((idx >> 6) % nblk), p = (int)((idx >> 6) / nblk);
+    const int col = 16 * p + (lane & 15), kb = 128 * b + 32 * (lane >> 4);
+    uint32_t w[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        uint32_t v = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int klo = kb + 8 * d + j, khi = klo + 4;
+            const uint32_t lo = (col < n && klo < k) ? (uint32_t)(q[(size_t)col * ldq + klo] + 8) : 8u;
+            const uint32_t hi = (col < n && khi < k) ? (uint32_t)(q[(size_t)col * ldq + khi] + 8) : 8u;
+            v |= ((lo & 15u) | ((hi & 15u) << 4)) << (8 * j);
+        }
+        w[d] = v;
+    }
+    *reinterpret_cast<uint4*>(codes + (size_t)p * nblk * 1024 + (size_t)b * 1024 + lane * 16) =
+        make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// int4 group scales s [n][lds] bf16 to [panel][k-block][kq][c]: the scale of column 16 p + c and group 4 b + kq
+__global__ __launch_bounds__(256) void dr_pack_int4_scales_k(const uint16_t* __restrict__ s, long long lds, int n,
+                                                             int k, uint16_t* __restrict__ out, int n_pad, int k_pad) {
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const int nblk = k_pad / 128;
+    if (idx >= (long long)(n_pad / 16) * nblk * 64) return;
+    const int lane = (int)(idx & 63), b = (int)((idx >> 6) % nblk), p = (int)((idx >> 6) / nblk);
+    const int col = 16 * p + (lane & 15), g = 4 * b + (lane >> 4);
+    out[idx] = (col < n && g < k / 32) ? s[(size_t)col * lds + g] : (uint16_t)0;
+}
+
 // ---- top-k merge -----------------------------------------------------------------------------------------------------
 //
 // Every slot of a row becomes a 64-bit key: the record's key (fp32 scores in key_f32's order, or the bf16 key as it
@@ -1075,6 +1198,9 @@ void launch_gemv(const Args& a, int grid, hipStream_t st) {
     switch (a.seg[0].fmt) {
         case DR_BFP8: hipLaunchKernelGGL((dr_gemv<MR, PW, DR_BFP8, true>), dim3(grid), b, lds, st, a); break;
         case DR_BFP4: hipLaunchKernelGGL((dr_gemv<MR, PW, DR_BFP4, true>), dim3(grid), b, lds, st, a); break;
+        case DR_INT4:
+            if constexpr (PW == 2 && MR <= 2) hipLaunchKernelGGL((dr_gemv<MR, PW, DR_INT4, true>), dim3(grid), b, lds, st, a);
+            break;
         default: hipLaunchKernelGGL((dr_gemv<MR, PW, DR_BF16, true>), dim3(grid), b, lds, st, a); break;
     }
 }
@@ -1113,10 +1239,34 @@ extern "C" {
 
 int64_t dr_codes_bytes(int fmt, int k_pad, int n_pad) {
     const int64_t v = (int64_t)k_pad * n_pad;
-    return fmt == DR_BFP8 ? v : fmt == DR_BFP4 ? v / 2 : 2 * v;
+    return fmt == DR_BFP8 ? v : (fmt == DR_BFP4 || fmt == DR_INT4) ? v / 2 : 2 * v;
 }
 
-int64_t dr_exps_bytes(int fmt, int k_pad, int n_pad) { return fmt == DR_BF16 ? 0 : (int64_t)k_pad * n_pad / 16; }
+int64_t dr_exps_bytes(int fmt, int k_pad, int n_pad) {
+    return (fmt == DR_BFP8 || fmt == DR_BFP4) ? (int64_t)k_pad * n_pad / 16 : 0;
+}
+
+int64_t dr_int4_scales_bytes(int k_pad, int n_pad) { return (int64_t)(k_pad / 128) * 4 * n_pad * 2; }
+
+int dr_pack_int4(const int8_t* q, int64_t ld_q, int n, int k, void* codes, int n_pad, int k_pad, void* stream) {
+    if (q == nullptr || codes == nullptr || n <= 0 || k <= 0 || k % 32 || n_pad < n || n_pad % 32 || k_pad < k ||
+        k_pad % KALIGN || ld_q < k)
+        return DR_EINVAL;
+    const long long threads = (long long)(n_pad / 16) * (k_pad / 128) * 64;
+    hipLaunchKernelGGL(dr_pack_int4_k, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, S(stream), q,
+                       (long long)ld_q, n, k, reinterpret_cast<uint8_t*>(codes), n_pad, k_pad);
+    return hip_status(hipGetLastError());
+}
+
+int dr_pack_int4_scales(const uint16_t* s, int64_t ld_s, int n, int k, void* out, int n_pad, int k_pad, void* stream) {
+    if (s == nullptr || out == nullptr || n <= 0 || k <= 0 || k % 32 || n_pad < n || n_pad % 32 || k_pad < k ||
+        k_pad % KALIGN || ld_s < k / 32)
+        return DR_EINVAL;
+    const long long threads = (long long)(n_pad / 16) * (k_pad / 128) * 64;
+    hipLaunchKernelGGL(dr_pack_int4_scales_k, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, S(stream), s,
+                       (long long)ld_s, n, k, reinterpret_cast<uint16_t*>(out), n_pad, k_pad);
+    return hip_status(hipGetLastError());
+}
 
 int dr_pack(const float* w, int64_t ld_w, int n, int k, int fmt, const float* col_div, void* codes, void* exps,
             int n_pad, int k_pad, void* stream) {
@@ -1192,9 +1342,12 @@ int prepare(const dr_launch* L, Args& a, int& pw, int& tiles, int& mr) {
     for (int i = 0; i < L->nseg; ++i) {
         const dr_segment& s = L->seg[i];
         SegDev& d = a.seg[i];
-        if (s.fmt < 0 || s.fmt > 2 || s.n <= 0 || s.n_pad < s.n || s.n_pad % 32 || s.col0 < 0 || s.col0 % 32 ||
-            s.codes == nullptr || (s.fmt != DR_BF16 && s.exps == nullptr) || s.glu < 0 || s.glu > 2 ||
-            (s.glu ? 4 : 2) != pw)
+        const bool bfp = s.fmt == DR_BFP8 || s.fmt == DR_BFP4;
+        if (s.fmt < 0 || s.fmt > 3 || s.n <= 0 || s.n_pad < s.n || s.n_pad % 32 || s.col0 < 0 || s.col0 % 32 ||
+            s.codes == nullptr || (bfp && s.exps == nullptr) || s.glu < 0 || s.glu > 2 || (s.glu ? 4 : 2) != pw)
+            return DR_EINVAL;
+        // an int4 weight alone: one segment, no GLU, residual or top-k, its group scales given
+        if (s.fmt == DR_INT4 && (L->nseg != 1 || s.glu || s.scale == nullptr || L->residual || L->topk.records))
             return DR_EINVAL;
         if (s.glu == 1 && s.n % 64) return DR_EINVAL;
         if (s.glu == 2 && (s.codes_up == nullptr || (s.fmt != DR_BF16 && s.exps_up == nullptr))) return DR_EINVAL;
@@ -1202,7 +1355,8 @@ int prepare(const dr_launch* L, Args& a, int& pw, int& tiles, int& mr) {
         d.exps = reinterpret_cast<const uint8_t*>(s.exps);
         d.codes_up = reinterpret_cast<const uint8_t*>(s.codes_up);
         d.exps_up = reinterpret_cast<const uint8_t*>(s.exps_up);
-        d.scale = s.scale;
+        d.scale = s.fmt == DR_INT4 ? nullptr : s.scale;
+        d.gscale = s.fmt == DR_INT4 ? reinterpret_cast<const uint16_t*>(s.scale) : nullptr;
         d.scale_up = s.scale_up;
         d.fmt = s.fmt;
         d.n = s.n;
@@ -1237,6 +1391,7 @@ int prepare(const dr_launch* L, Args& a, int& pw, int& tiles, int& mr) {
     mr = rows_per_pass(L->m);
     if (pw == 4 && mr == 8) mr = 4;    // (GLU: at most 4 GEMV rows or 16 MFMA rows a pass, for the registers
     if (pw == 4 && mr == 32) mr = 16;  // and the LDS)
+    if (a.seg[0].fmt == DR_INT4) mr = L->m >= 2 ? 2 : 1;  // (int4: the GEMV, two rows a pass)
     return DR_OK;
 }
 

@@ -204,3 +204,32 @@ def test_bf16_ceil_and_interleave():
     u = -g
     iv = O.interleave_glu(g, u)
     assert torch.equal(iv[:32], g[:32]) and torch.equal(iv[32:64], u[:32]) and torch.equal(iv[64:96], g[32:])
+
+
+def test_int4_layout_decodes_to_codes():
+    """The oracle's int4 layout, decoded with the bfloat4_b address formula above at exponent 129 (m * 2^0 = q), gives
+    the codes back; zeros past N and K; the scale order puts column 16 p + c, group 4 b + kq at [p][b][kq][c]."""
+    g = torch.Generator().manual_seed(21)
+    n, k, n_pad = 40, 96, 64
+    codes = torch.randint(-7, 8, (n, k), generator=g).numpy()
+    lay = O.int4_layout(codes, n_pad, 256)
+    exps = np.full(n_pad // 16 * 256, 129, np.uint8)
+    got = _unlayout(lay, exps, "bfp4", k, n, n_pad)
+    assert np.array_equal(got, codes.T.astype(np.float32))
+    s = (torch.arange(n * (k // 32), dtype=torch.int64).reshape(n, k // 32) + 1).numpy().astype(np.uint16)
+    sl = O.int4_scales_layout(s, n_pad, 256).reshape(n_pad // 16, 2, 4, 16)
+    for col in (0, 17, 39):
+        for grp in range(k // 32):
+            p, c = divmod(col, 16)
+            b, kq = divmod(grp, 4)
+            assert sl[p, b, kq, c] == s[col, grp]
+    assert sl[2, 0, 0, 9] == 0 and sl[0, 0, 3, 0] == 0  # column 41 (past N), group 3 (past K)
+
+
+def test_int4_nibbles_matches_reference_format():
+    """w4a16.nibbles (the reference's tile bytes, reshape form) against the oracle's element-by-element restatement."""
+    from int4 import w4a16
+
+    g = torch.Generator().manual_seed(22)
+    codes = torch.randint(-7, 8, (64, 96), generator=g).to(torch.int8)  # [K, N]
+    assert np.array_equal(w4a16.nibbles(codes).numpy(), O.int4_nibbles(codes.numpy()))

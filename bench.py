@@ -1,6 +1,6 @@
 """Benchmark of the dense_reader decode matmul on one MI355X.
 
-  python bench.py [--steps K] [--warmup W] [--config ns|c1|c2|c3|c4|c5] [--no-cpu] [--cpu-seconds S]
+  python bench.py [--steps K] [--warmup W] [--config ns|c1|c2|c3|c4|c5|int4|lm] [--no-cpu] [--cpu-seconds S]
   python bench.py --copy-probe      (a plain 256 MiB copy kernel: the byte counters' calibration under rocprofv3)
 
 Default workload: the north-star decode matmul, bfloat8_b M=1, x [1, 4096] bf16 @ W [4096 in, 14336 out] (W ~
@@ -10,7 +10,8 @@ serve them. The K timed steps are captured once in a HIP graph (the analogue of 
 replayed between synchronisations; events on the replay stream bracket the timed region. One JSON line on stdout:
 
   value             algorithmic weight bytes per step (the reference's 1088 / 576 / 2048 B per 32x32 tile of
-                    bfloat8_b / bfloat4_b / bfloat16) x steps / timed seconds, GB/s, inputs resident in HBM;
+                    bfloat8_b / bfloat4_b / bfloat16; int4: 512 B of codes and 64 B of bf16 group scales) x steps /
+                    timed seconds, GB/s, inputs resident in HBM;
   roofline.achieved the same bytes per matmul launch / that kernel's mean duration (a graph of K launches of the
                     matmul alone, timed the same way; the step itself when it is one launch);
   roofline.traffic  HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE runs (profiles/traffic.md), scaled by
@@ -62,6 +63,13 @@ CONFIGS = {
         4096,
         [(128256, "bfp8", False)],
         {"topk": True},
+    ),
+    "int4": (
+        "int4 W4A16 M=1 K=4096 N=14336: codes -7..7 with a bf16 scale per column and 32 inputs (int4 w4a16_linear)",
+        1,
+        4096,
+        [(14336, "int4", True)],
+        {"int4": True},
     ),
     "lm": (
         "LM head to token ids, M=4 K=4096 vocab=128256 bfp8: bf16 top-8 records, the best 16 rescored from the bf16 "
@@ -126,7 +134,16 @@ class Workload:
         self.x = torch.randn(m, k, generator=g, device="cuda").to(torch.bfloat16).reshape(1, 1, m, k)
 
         self.heads = None
-        if o.get("lmhead"):
+        if o.get("int4"):
+            from int4 import w4a16
+
+            def make():
+                n = ws[0][0]
+                codes = torch.randint(-7, 8, (n, k), generator=g, device="cuda", dtype=torch.int8)
+                scales = (torch.rand(n, k // 32, generator=g, device="cuda") * 0.01 + 0.001).to(torch.bfloat16)
+                return [Int4Set(w4a16, dev, codes, scales)]
+
+        elif o.get("lmhead"):
             from lm_head_topk import lmhead
 
             def make():
@@ -152,7 +169,8 @@ class Workload:
         else:
             self.sets = [first] + [make() for _ in range(self.copies - 1)]
         self.scales = [
-            linear.scale_tensor(dev, torch.rand(n, generator=g, device="cuda") + 0.5, dtype=linear.float32) if sc else None
+            linear.scale_tensor(dev, torch.rand(n, generator=g, device="cuda") + 0.5, dtype=linear.float32)
+            if sc and not o.get("int4") else None
             for n, _, sc in ws
         ]
         self.n = ws[0][0] if (o.get("glu2")) else sum(n for n, _, _ in ws)
@@ -182,6 +200,8 @@ class Workload:
                 h.logits_topk(self.x, self.m)  # (the result tensor, made once outside any graph)
             spec = {"r": h.results[self.m], "k": h.k, "rows": self.m, "slot0": 0, "base": 0, "n": h.step, "write_y": False}
             L.matmul(self.x, ws[0], None, out=h.y, topk=spec)
+        elif o.get("int4"):
+            ws[0].w4a16.w4a16_linear(self.x, ws[0].wq, ws[0].ts)
         elif self.res is not None:
             L.matmul(self.x, ws[0], None, residual=self.res, out32=True)  # (fp32 out: a fresh output each call)
         else:
@@ -194,6 +214,21 @@ class Workload:
         self.kernel(i)
         if self.o.get("topk"):
             self.linear.topk_merge(self.rec, self.m, 8, k_out=32, fp32=True)
+
+
+class Int4Set:
+    """An int4 weight and its group scales on the GPU (int4.w4a16), with the byte counts the bench reports."""
+
+    def __init__(self, w4a16, dev, codes, scales):
+        self.w4a16, self.codes, self.scales = w4a16, codes, scales
+        self.wq = w4a16.int4_weight(dev, codes)
+        self.ts = w4a16.group_scales(dev, scales)
+
+    def algorithmic_bytes(self):
+        return self.w4a16.algorithmic_bytes(self.wq)
+
+    def nbytes(self):
+        return self.wq["t"].numel() + 2 * self.ts.numel()
 
 
 def timed_graph(torch, fn, steps):
@@ -308,7 +343,10 @@ def cpu_baseline(wl, seconds):
     torch.set_num_threads(threads)
     m, o = wl.m, wl.o
     xc = wl.x.reshape(m, -1).cpu()
-    hw = [wl.linear.held(w).cpu().contiguous() for w in wl.sets[0]]
+    if o.get("int4"):  # the reference's host check: x (bf16) @ (q * s).T in float32 (int4/w4a16.py:100-107)
+        hw = [O.int4_dequantized(w.codes.cpu(), w.scales.cpu()).float().T.contiguous() for w in wl.sets[0]]
+    else:
+        hw = [wl.linear.held(w).cpu().contiguous() for w in wl.sets[0]]
     sc = [s.float().cpu().reshape(-1) if s is not None else None for s in wl.scales]
     rc = wl.res.reshape(m, -1).float().cpu() if wl.res is not None else None
 
@@ -342,7 +380,8 @@ def cpu_baseline(wl, seconds):
         "us_per_call": round(med * 1e6, 1),
         "cores": threads,
         "kind": "port",
-        "sample": f"{len(times)} calls (median) of oracle.ref_f32 (x bf16->f32 @ held W f32) plus the epilogue, "
+        "sample": f"{len(times)} calls (median) of oracle.ref_f32 (x bf16->f32 @ held W f32; int4: W = q * s) plus "
+        "the epilogue, "
         f"the full config shapes, {threads} threads, ~{seconds:.0f} s",
     }
 

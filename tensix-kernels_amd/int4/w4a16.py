@@ -91,6 +91,12 @@ def plan(device, wq, cores_per_bank=3, kb=None, kw=None, sbw=None, full_sync=Tru
     return {"chunks": chunks, "kch": kch, "tiles": -(-wq["n"] // TILE), "rows_per_pass": rows}
 
 
+def algorithmic_bytes(wq):
+    """The reference's bytes of an int4 weight: a 512-byte tile of codes per 32 x 32 values and their bf16 group
+    scales, 64 bytes a tile (its [K / 32, N] scale tensor)."""
+    return (wq["k"] // TILE) * -(-wq["n"] // TILE) * (Q4_TILE + 2 * TILE)
+
+
 def w4a16_linear(x, wq, scale, *, memory_config=None, fidelity="hifi2", **opts):
     """y = x @ (q * s).T for one token: x [1, 1, 1, K] bf16 on the GPU, wq from int4_weight, scale from group_scales.
     Returns [1, 1, 1, N] bf16. opts (the reference's Tensix work split) change nothing (reference

@@ -233,3 +233,20 @@ def test_int4_nibbles_matches_reference_format():
     g = torch.Generator().manual_seed(22)
     codes = torch.randint(-7, 8, (64, 96), generator=g).to(torch.int8)  # [K, N]
     assert np.array_equal(w4a16.nibbles(codes).numpy(), O.int4_nibbles(codes.numpy()))
+
+
+def test_int4_ref_hand_case():
+    """int4_dequantized and int4_ref on a hand-worked case: the scale 0.1 held as the bf16 0.10009765625, q * s per
+    group of 32 inputs, x rounded to bf16 first (1 + 2^-10 is 1 in bf16)."""
+    codes = np.zeros((2, 64), np.int8)
+    codes[0, :32], codes[0, 32:] = 1, -7
+    codes[1, 0::2], codes[1, 1::2] = 3, -2
+    scales = torch.tensor([[0.1, 2.0], [0.5, 0.25]])
+    w = O.int4_dequantized(codes, scales)
+    assert float(w[0, 0]) == 0.10009765625 and float(w[0, 40]) == -14.0
+    assert float(w[1, 1]) == -1.0 and float(w[1, 33]) == -0.5 and float(w[1, 32]) == 0.75
+    x = torch.ones(1, 64)
+    x[0, 0] = 1.0009765625
+    y = O.int4_ref(x, codes, scales)
+    # row 0: 32 * 0.10009765625 - 32 * 7 * 2; row 1: 16 * (3 - 2) * 0.5 + 16 * (3 - 2) * 0.25
+    assert y.tolist() == [[-444.796875, 12.0]]

@@ -1,4 +1,5 @@
-"""ctypes binding of libdense_reader.so (the C ABI declared in include/dense_reader.h and include/lm_head.h).
+"""ctypes binding of libdense_reader.so (the C ABI declared in include/dense_reader.h, include/lm_head.h and
+include/moe.h).
 
 The library is built in-tree (`python -c "import __graft_entry__; __graft_entry__.build()"` at the repository root,
 or `make -C tensix-kernels_amd/dense_reader/csrc`). There is no fallback: without the library every op raises.
@@ -13,7 +14,7 @@ LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
 DR_OK, DR_EINVAL, DR_EHIP, DR_ERANGE = 0, 1, 2, 3
 
-# every symbol include/dense_reader.h and include/lm_head.h declare
+# every symbol include/dense_reader.h, include/lm_head.h and include/moe.h declare
 SYMBOLS = (
     "dr_codes_bytes",
     "dr_exps_bytes",
@@ -31,7 +32,12 @@ SYMBOLS = (
     "dr_version",
     "dr_head_pick",
     "dr_head_pick_records",
+    "dr_moe_workspace_bytes",
+    "dr_moe_matmul",
+    "dr_moe_route",
 )
+
+DR_MOE_GATE_UP, DR_MOE_DOWN, DR_MOE_GATE_UP_ROWS, DR_MOE_DOWN_ROWS = 1, 2, 3, 4
 
 c_int, c_int32, c_int64, c_void_p = ctypes.c_int, ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p
 
@@ -89,6 +95,50 @@ class Launch(ctypes.Structure):
     ]
 
 
+class Moe(ctypes.Structure):
+    _fields_ = [
+        ("mode", c_int32),
+        ("ids", c_void_p),
+        ("ids32", c_int32),
+        ("ld_ids", c_int32),
+        ("slots", c_int32),
+        ("id_rows", c_int32),
+        ("experts", c_int32),
+        ("w", c_void_p),
+        ("ld_w", c_int32),
+        ("expert_n", c_int32),
+        ("expert_k", c_int32),
+        ("codes_stride", c_int64),
+        ("exps_stride", c_int64),
+        ("bias", c_void_p),
+    ]
+
+
+class Route(ctypes.Structure):
+    _fields_ = [
+        ("logits", c_void_p),
+        ("rows", c_int32),
+        ("ld_logits", c_int32),
+        ("experts", c_int32),
+        ("k", c_int32),
+        ("kind", c_int32),
+        ("bias", c_void_p),
+        ("ids", c_void_p),
+        ("ids32", c_int32),
+        ("ld_ids", c_int32),
+        ("w", c_void_p),
+        ("ld_w", c_int32),
+        ("shared", c_void_p),
+        ("ld_shared", c_int32),
+        ("scale", ctypes.c_double),
+        ("norm", c_int32),
+        ("n_group", c_int32),
+        ("topk_group", c_int32),
+        ("slot", c_int64),
+        ("stream", c_void_p),
+    ]
+
+
 _lib = None
 
 
@@ -138,6 +188,12 @@ def lib():
         L.dr_head_pick_records.restype = c_int
         L.dr_head_pick_records.argtypes = [c_void_p, c_int, c_int, c_int, c_int64, c_void_p, c_void_p, c_void_p,
                                            c_void_p, c_int64, c_void_p]
+        L.dr_moe_workspace_bytes.restype = c_int64
+        L.dr_moe_workspace_bytes.argtypes = [ctypes.POINTER(Launch), ctypes.POINTER(Moe)]
+        L.dr_moe_matmul.restype = c_int
+        L.dr_moe_matmul.argtypes = [ctypes.POINTER(Launch), ctypes.POINTER(Moe)]
+        L.dr_moe_route.restype = c_int
+        L.dr_moe_route.argtypes = [ctypes.POINTER(Route)]
         _lib = L
     return _lib
 

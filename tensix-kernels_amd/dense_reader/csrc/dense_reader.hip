@@ -28,6 +28,7 @@
 #include <stdint.h>
 
 #include "dense_reader.h"
+#include "moe.h"
 #include "wave_select.h"
 
 // No contraction of a multiply and an add into an FMA unless the code asks for one: the compiler would otherwise
@@ -97,6 +98,15 @@ struct Args {
     int splits, cps, tiles;  // split K: splits workgroups a tile, cps chunks each; tiles of the launch
     uint32_t* counters;      // [tiles] (splits > 1): workgroups of the tile done, reset to 0 by the last
     float* wpart;            // [tiles][splits][PW * ROWS * 16] (splits > 1): each workgroup's column sums
+    // expert gather (DR_MOE_*): the workgroup's expert (gate/up modes) or each chunk's (down modes), read from ids
+    const void* ids;
+    int ids32, ld_ids, slots, id_rows, experts;
+    const uint16_t* rw;  // routing weights [id_rows][ld_rw] bf16
+    int ld_rw;
+    int en, tpe;         // gate/up modes: an expert's output columns, its 32-column tiles
+    int ek, ekp;         // down modes: an expert's rows (x's block width) and the rows packed (a multiple of 256)
+    long long cstride, estride;  // bytes from one expert's codes / exponents to the next
+    const uint16_t* bias;        // gate/up modes: [experts][2][en] bf16 (gate, up) or null
 };
 
 // ---- the K loop of one wavefront: partial sums of PW panels x MR rows over [k0, k1) ------------------------------
@@ -412,10 +422,17 @@ __device__ __forceinline__ float load_scale(const void* s, int f32, int col) {
     return f32 ? reinterpret_cast<const float*>(s)[col] : bf16_to_f32(reinterpret_cast<const uint16_t*>(s)[col]);
 }
 
-__device__ __forceinline__ float act_glu(float g, int act) {
-    // silu(g) = g * sigmoid(g); gelu_tanh(g) = g * sigmoid(1.5957691216 g + 0.0713548162 g^3) (dense_ops.h:46-59)
-    const float z = act == 1 ? g * (1.5957691216f + 0.0713548162f * (g * g)) : g;
-    return g / (1.f + __expf(-z));
+// act(g) * u: silu(g) = g * sigmoid(g); gelu_tanh(g) = g * sigmoid(1.5957691216 g + 0.0713548162 g^3)
+// (dense_ops.h:46-59); swiglu_oai min(g, 7) * sigmoid(1.702 min(g, 7)) * (clamp(u, -7, 7) + 1) (dense_ops.h:90-118),
+// a NaN passing through the clamps as it does there
+__device__ __forceinline__ float glu(float g, float u, int act) {
+    if (act == DR_ACT_SWIGLU_OAI) {
+        const float gc = g > 7.f ? 7.f : g;
+        const float uc = u > 7.f ? 7.f : (u < -7.f ? -7.f : u);
+        return gc / (1.f + __expf(-(1.702f * gc))) * (uc + 1.f);
+    }
+    const float z = act == DR_ACT_GELU_TANH ? g * (1.5957691216f + 0.0713548162f * (g * g)) : g;
+    return g / (1.f + __expf(-z)) * u;
 }
 
 // the reference's top-k key of a bf16 (dense_writer.cpp:215): a monotonic uint16, 0 below everything
@@ -423,6 +440,54 @@ __device__ __forceinline__ uint32_t key_bf16(uint32_t b) { return b ^ (0x8000u |
 __device__ __forceinline__ uint32_t key_f32(float f) {
     const uint32_t u = __float_as_uint(f);
     return u ^ ((u >> 31) ? 0xFFFFFFFFu : 0x80000000u);
+}
+
+// ---- expert gather: ids, the union of the rows' ids ----------------------------------------------------------------
+
+// expert id j of row r, or -1 when it is not below the expert count (it chooses nothing)
+__device__ __forceinline__ int moe_id(const Args& a, int r, int j) {
+    const size_t i = (size_t)r * a.ld_ids + j;
+    const uint32_t e = a.ids32 ? reinterpret_cast<const uint32_t*>(a.ids)[i] : reinterpret_cast<const uint16_t*>(a.ids)[i];
+    return e < (uint32_t)a.experts ? (int)e : -1;
+}
+
+// the distinct ids below the expert count of the ids' rows, in increasing order (moe/kernels/moe8_rows.h's union)
+struct UnionLds {
+    uint32_t bits[32];
+    uint16_t list[1024];
+    int count;
+};
+
+template <int MOE>
+__device__ __forceinline__ UnionLds* union_lds() {
+    __shared__ UnionLds u;
+    return &u;
+}
+
+// every thread of the workgroup calls it: a bitmap of the ids, then wavefront 0 lists its set bits in order
+__device__ __forceinline__ void moe_union(const Args& a, UnionLds& u) {
+    for (int i = threadIdx.x; i < 32; i += blockDim.x) u.bits[i] = 0u;
+    __syncthreads();
+    for (int i = threadIdx.x; i < a.id_rows * a.slots; i += blockDim.x) {
+        const int e = moe_id(a, i / a.slots, i % a.slots);
+        if (e >= 0) atomicOr(&u.bits[e >> 5], 1u << (e & 31));
+    }
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        const int l = threadIdx.x;
+        const uint32_t w = l < 32 ? u.bits[l] : 0u;
+        const int c = __popc(w);
+        int incl = c;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int v = __shfl_up(incl, o);
+            if (l >= o) incl += v;
+        }
+        int pos = incl - c;
+        for (uint32_t m = w; m != 0u; m &= m - 1u) u.list[pos++] = (uint16_t)(32 * l + __ffs(m) - 1);
+        if (l == 63) u.count = incl;
+    }
+    __syncthreads();
 }
 
 // ---- the workgroup's tile: its segment, its panels -------------------------------------------------------------------
@@ -496,7 +561,7 @@ __device__ __forceinline__ void epilogue(const Args& a, const SegDev& sg, int t,
                     suv = load_scale(sg.scale_up, sg.scale_f32, oc);
                 }
             }
-            v = act_glu(gsum * sgv, a.act) * (usum * suv);
+            v = glu(gsum * sgv, usum * suv, a.act);
         } else {
             const size_t ycol = (size_t)sg.col0 + oc;
             if (valid && a.res != nullptr && a.res_mode == 2) v = bf16_to_f32(a.res[(size_t)m * a.ldr + ycol]);
@@ -556,6 +621,55 @@ __device__ __forceinline__ void epilogue(const Args& a, const SegDev& sg, int t,
     }
 }
 
+// the gate/up modes' epilogue: thread (m, col) of the tile adds the bias, applies the GLU and the row's routing weight
+// for the expert (the slot's in DR_MOE_GATE_UP; 0 where the row did not choose it in DR_MOE_GATE_UP_ROWS) and writes
+// the unit's columns of y (moe_gu_compute.cpp: the GLU in dest, then times the weight's tile)
+template <int ROWS, int MOE>
+__device__ __forceinline__ void epilogue_moe(const Args& a, int t, int unit, int ex, const float* part, int nparts) {
+    constexpr int PW = 4;
+    __shared__ float coef[ROWS];
+    const int mrows = min(a.m, ROWS);
+    if (threadIdx.x < ROWS) {
+        const int m = threadIdx.x, r = a.row0 + m;
+        float c = 0.f;
+        if (m < mrows) {
+            if (MOE == DR_MOE_GATE_UP) {
+                c = bf16_to_f32(a.rw[unit]);
+            } else if (r < a.id_rows) {
+                for (int j = 0; j < a.slots; ++j)
+                    if (moe_id(a, r, j) == ex) c = bf16_to_f32(a.rw[(size_t)r * a.ld_rw + j]);
+            }
+        }
+        coef[m] = c;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < TILE * ROWS; e += blockDim.x) {
+        const int m = e / TILE, col = e % TILE;
+        const int oc = t * TILE + col;  // the column within the expert's
+        if (m >= mrows || oc >= a.en) continue;
+        const int cq = col >> 4, cc = col & 15;
+        float gsum = 0.f, usum = 0.f;
+        for (int w = 0; w < nparts; ++w) {
+            gsum += part[((w * PW + cq) * ROWS + m) * 16 + cc];
+            usum += part[((w * PW + 2 + cq) * ROWS + m) * 16 + cc];
+        }
+        if (a.bias != nullptr) {
+            gsum += bf16_to_f32(a.bias[((size_t)ex * 2 + 0) * a.en + oc]);
+            usum += bf16_to_f32(a.bias[((size_t)ex * 2 + 1) * a.en + oc]);
+        }
+        const float v = glu(gsum, usum, a.act) * coef[m];
+        reinterpret_cast<uint16_t*>(a.y)[(size_t)m * a.ldy + (size_t)unit * a.en + oc] = (uint16_t)f32_to_bf16(v);
+    }
+}
+
+// DR_MOE_GATE_UP with an id past the experts: the slot's columns of this tile are zeros
+__device__ __forceinline__ void moe_zero(const Args& a, int t, int unit) {
+    for (int col = threadIdx.x; col < TILE; col += blockDim.x) {
+        const int oc = t * TILE + col;
+        if (oc < a.en) reinterpret_cast<uint16_t*>(a.y)[(size_t)unit * a.en + oc] = 0;
+    }
+}
+
 // ---- split K: the tile's workgroups meet in the workspace ------------------------------------------------------------
 //
 // With splits > 1 each of a tile's workgroups takes cps chunks; it adds its wavefronts' sums (in order), writes them
@@ -603,8 +717,23 @@ __device__ __forceinline__ int gather_splits(const Args& a, int g, int split, fl
 // ---- the GEMV kernel (few rows): VALU decode and FMA, one accumulator a lane per panel and row -----------------------
 //
 // FMT >= 0: every segment has that format (one K loop compiled in: a smaller kernel); FMT < 0: each workgroup
-// branches on its segment's format. ONE: a single segment.
-template <int MR, int PW, int FMT, bool ONE>
+// branches on its segment's format. ONE: a single segment. MOE: an expert gather (DR_MOE_*, bfloat4_b, one segment)
+// or 0.
+//
+// The expert gather. Gate/up modes: the launch's tiles are units (slots, or the union's experts) times the expert's
+// tiles; the workgroup's unit gives its expert, whose weights sit cstride / estride bytes per expert further on.
+// Down modes: the launch's K is the units' blocks of ekp rows one after another; a chunk lies in one unit (ekp is a
+// multiple of the chunk), whose expert gives that chunk's weights and whose ek values of x sit at unit * ek.
+template <int MOE>
+__device__ __forceinline__ constexpr bool moe_k() {
+    return MOE == DR_MOE_DOWN || MOE == DR_MOE_DOWN_ROWS;
+}
+template <int MOE>
+__device__ __forceinline__ constexpr bool moe_n() {
+    return MOE == DR_MOE_GATE_UP || MOE == DR_MOE_GATE_UP_ROWS;
+}
+
+template <int MR, int PW, int FMT, bool ONE, int MOE = 0>
 __global__ __launch_bounds__(512) void dr_gemv(const Args a) {
     extern __shared__ float part[];  // [W][PW][MR][16]
     __shared__ float tval[MR][TILE];
@@ -612,42 +741,64 @@ __global__ __launch_bounds__(512) void dr_gemv(const Args a) {
 
     const int g = blockIdx.x % a.tiles, split = blockIdx.x / a.tiles;
     const SegDev& sg = a.seg[find_segment<ONE>(a, g)];
-    const int t = g - sg.tile_begin;
+    int t = g - sg.tile_begin;
     // (the wavefront index is uniform across the wavefront; readfirstlane lets the compiler see it, so the chunk
     // bounds and loop trip counts live in SGPRs and the K loops branch on scalars)
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int fmt = FMT >= 0 ? FMT : sg.fmt;
+    UnionLds* ul = nullptr;
+    if constexpr (MOE == DR_MOE_GATE_UP_ROWS || MOE == DR_MOE_DOWN_ROWS) {
+        ul = union_lds<MOE>();
+        moe_union(a, *ul);
+    }
+    int unit = 0, ex = 0;
+    if constexpr (moe_n<MOE>()) {
+        unit = t / a.tpe;
+        t -= unit * a.tpe;
+        ex = MOE == DR_MOE_GATE_UP ? moe_id(a, 0, unit) : (unit < ul->count ? (int)ul->list[unit] : -1);
+        ex = __builtin_amdgcn_readfirstlane(ex);
+        if (ex < 0) {
+            if (MOE == DR_MOE_GATE_UP && split == 0) moe_zero(a, t, unit);
+            return;
+        }
+    }
     const uint8_t* cb[PW];
     const uint8_t* eb[PW];
-    panel_ptrs<PW>(sg, t, a.k_pad, cb, eb);
+    panel_ptrs<PW>(sg, t, moe_k<MOE>() ? a.ekp : a.k_pad, cb, eb);
+    if constexpr (moe_n<MOE>()) {
+#pragma unroll
+        for (int q = 0; q < PW; ++q) {
+            cb[q] += (size_t)ex * a.cstride;
+            eb[q] += (size_t)ex * a.estride;
+        }
+    }
 
     float wsum[PW][MR];  // this wavefront's column sums (lanes 0..15), its chunks added in order
 #pragma unroll
     for (int q = 0; q < PW; ++q)
 #pragma unroll
         for (int m = 0; m < MR; ++m) wsum[q][m] = 0.f;
-    const int ch1 = min((split + 1) * a.cps, a.chunks);
-    for (int ch = split * a.cps + wave; ch < ch1; ch += a.waves) {
+    // one chunk [k0, k1) of x (b) against the panels cbx / ebx, added to wsum
+    auto chunk = [&](const Args& b, const uint8_t* const* cbx, const uint8_t* const* ebx, int k0, int k1) {
         float acc[PW][MR], corr[PW][MR];
 #pragma unroll
         for (int q = 0; q < PW; ++q)
 #pragma unroll
             for (int m = 0; m < MR; ++m) acc[q][m] = corr[q][m] = 0.f;
-        const int k0 = ch * a.kch, k1 = min(k0 + a.kch, a.k_pad);
         if (fmt == DR_BFP8) {
-            chunk_bfp8<MR, PW>(a, cb, eb, k0, k1, lane, acc);
+            chunk_bfp8<MR, PW>(b, cbx, ebx, k0, k1, lane, acc);
         } else if (FMT == DR_INT4) {
             const uint16_t* gs[PW];
 #pragma unroll
-            for (int q = 0; q < PW; ++q) gs[q] = sg.gscale + (size_t)(2 * t + q) * (a.k_pad / 128) * 64;
-            chunk_int4<MR, PW>(a, cb, gs, k0, k1, lane, acc);
+            for (int q = 0; q < PW; ++q) gs[q] = sg.gscale + (size_t)(2 * t + q) * (b.k_pad / 128) * 64;
+            chunk_int4<MR, PW>(b, cbx, gs, k0, k1, lane, acc);
         } else if (fmt == DR_BFP4) {
             float sx[PW][MR];
 #pragma unroll
             for (int q = 0; q < PW; ++q)
 #pragma unroll
                 for (int m = 0; m < MR; ++m) sx[q][m] = 0.f;
-            chunk_bfp4<MR, PW>(a, cb, eb, k0, k1, lane, acc, sx);
+            chunk_bfp4<MR, PW>(b, cbx, ebx, k0, k1, lane, acc, sx);
             // the wavefront's 136 * sum x' (every lane made distinct x'), taken off every column
 #pragma unroll
             for (int q = 0; q < PW; ++q)
@@ -659,7 +810,7 @@ __global__ __launch_bounds__(512) void dr_gemv(const Args a) {
                     corr[q][m] = 136.f * v;
                 }
         } else {
-            chunk_bf16<MR, PW>(a, cb, k0, k1, lane, acc);
+            chunk_bf16<MR, PW>(b, cbx, k0, k1, lane, acc);
         }
         // the chunk's column sums: the four quarter-rows of each column, in a fixed order
 #pragma unroll
@@ -671,6 +822,30 @@ __global__ __launch_bounds__(512) void dr_gemv(const Args a) {
                 v += __shfl_xor(v, 32);
                 wsum[q][m] += v - corr[q][m];
             }
+    };
+    const int ch1 = min((split + 1) * a.cps, a.chunks);
+    for (int ch = split * a.cps + wave; ch < ch1; ch += a.waves) {
+        const int k0 = ch * a.kch, k1 = min(k0 + a.kch, a.k_pad);
+        if constexpr (moe_k<MOE>()) {
+            const int s = k0 / a.ekp;
+            int e = MOE == DR_MOE_DOWN ? moe_id(a, 0, s) : (s < ul->count ? (int)ul->list[s] : -1);
+            e = __builtin_amdgcn_readfirstlane(e);
+            if (e < 0) continue;  // (an id past the experts, or a block past the union: nothing to add)
+            Args b = a;
+            b.x = a.x + (size_t)s * a.ek;
+            b.k = a.ek;
+            b.k_pad = a.ekp;
+            const uint8_t* cbe[PW];
+            const uint8_t* ebe[PW];
+#pragma unroll
+            for (int q = 0; q < PW; ++q) {
+                cbe[q] = cb[q] + (size_t)e * a.cstride;
+                ebe[q] = eb[q] + (size_t)e * a.estride;
+            }
+            chunk(b, cbe, ebe, k0 - s * a.ekp, k1 - s * a.ekp);
+        } else {
+            chunk(a, cb, eb, k0, k1);
+        }
     }
     if (lane < 16) {
 #pragma unroll
@@ -680,7 +855,11 @@ __global__ __launch_bounds__(512) void dr_gemv(const Args a) {
     }
     __syncthreads();
     const int nparts = gather_splits<MR, PW>(a, g, split, part);
-    if (nparts) epilogue<MR, PW>(a, sg, t, part, nparts, tval, tkey, wave, lane);
+    if (!nparts) return;
+    if constexpr (moe_n<MOE>())
+        epilogue_moe<MR, MOE>(a, t, unit, ex, part, nparts);
+    else
+        epilogue<MR, PW>(a, sg, t, part, nparts, tval, tkey, wave, lane);
 }
 
 // ---- the MFMA kernel (rows in tiles of 16): 16x16x32 bf16 matrix cores, weights decoded to exact bf16 ---------------
@@ -896,7 +1075,7 @@ __device__ __forceinline__ void mgroup_bf16(const Args& a, const uint8_t* const*
             for (int tt = 0; tt < MT; ++tt) acc[q][tt] = mfma(A[u][tt], c[u][q], acc[q][tt]);
 }
 
-template <int MT, int PW, int FMT, bool ONE>
+template <int MT, int PW, int FMT, bool ONE, int MOE = 0>
 __global__ __launch_bounds__(512) void dr_mfma(const Args a) {
     constexpr int ROWS = 16 * MT;
     extern __shared__ float part[];  // [W][PW][ROWS][16]
@@ -905,27 +1084,73 @@ __global__ __launch_bounds__(512) void dr_mfma(const Args a) {
 
     const int g = blockIdx.x % a.tiles, split = blockIdx.x / a.tiles;
     const SegDev& sg = a.seg[find_segment<ONE>(a, g)];
-    const int t = g - sg.tile_begin;
+    int t = g - sg.tile_begin;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int fmt = FMT >= 0 ? FMT : sg.fmt;
+    // the expert gather, as dr_gemv's (only the rows modes take more than two rows)
+    UnionLds* ul = nullptr;
+    if constexpr (MOE == DR_MOE_GATE_UP_ROWS || MOE == DR_MOE_DOWN_ROWS) {
+        ul = union_lds<MOE>();
+        moe_union(a, *ul);
+    }
+    int unit = 0, ex = 0;
+    if constexpr (moe_n<MOE>()) {
+        unit = t / a.tpe;
+        t -= unit * a.tpe;
+        ex = MOE == DR_MOE_GATE_UP ? moe_id(a, 0, unit) : (unit < ul->count ? (int)ul->list[unit] : -1);
+        ex = __builtin_amdgcn_readfirstlane(ex);
+        if (ex < 0) {
+            if (MOE == DR_MOE_GATE_UP && split == 0) moe_zero(a, t, unit);
+            return;
+        }
+    }
     const uint8_t* cb[PW];
     const uint8_t* eb[PW];
-    panel_ptrs<PW>(sg, t, a.k_pad, cb, eb);
+    panel_ptrs<PW>(sg, t, moe_k<MOE>() ? a.ekp : a.k_pad, cb, eb);
+    if constexpr (moe_n<MOE>()) {
+#pragma unroll
+        for (int q = 0; q < PW; ++q) {
+            cb[q] += (size_t)ex * a.cstride;
+            eb[q] += (size_t)ex * a.estride;
+        }
+    }
 
     f32x4 acc[PW][MT];  // this wavefront's sums over its chunks, in order
 #pragma unroll
     for (int q = 0; q < PW; ++q)
 #pragma unroll
         for (int tt = 0; tt < MT; ++tt) acc[q][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto chunk = [&](const Args& b, const uint8_t* const* cbx, const uint8_t* const* ebx, int k0, int k1) {
+        if (fmt == DR_BFP8) {
+            for (int gg = k0 >> 8; gg < (k1 >> 8); ++gg) mgroup_bfp8<MT, PW>(b, cbx, ebx, gg, lane, acc);
+        } else if (fmt == DR_BFP4) {
+            for (int gg = k0 >> 8; gg < (k1 >> 8); ++gg) mgroup_bfp4<MT, PW>(b, cbx, ebx, gg, lane, acc);
+        } else {
+            for (int b0 = k0 / 32; b0 < k1 / 32; b0 += 4) mgroup_bf16<MT, PW>(b, cbx, b0, lane, acc);
+        }
+    };
     const int ch1 = min((split + 1) * a.cps, a.chunks);
     for (int ch = split * a.cps + wave; ch < ch1; ch += a.waves) {
         const int k0 = ch * a.kch, k1 = min(k0 + a.kch, a.k_pad);
-        if (fmt == DR_BFP8) {
-            for (int gg = k0 >> 8; gg < (k1 >> 8); ++gg) mgroup_bfp8<MT, PW>(a, cb, eb, gg, lane, acc);
-        } else if (fmt == DR_BFP4) {
-            for (int gg = k0 >> 8; gg < (k1 >> 8); ++gg) mgroup_bfp4<MT, PW>(a, cb, eb, gg, lane, acc);
+        if constexpr (moe_k<MOE>()) {
+            const int s = k0 / a.ekp;
+            int e = MOE == DR_MOE_DOWN ? moe_id(a, 0, s) : (s < ul->count ? (int)ul->list[s] : -1);
+            e = __builtin_amdgcn_readfirstlane(e);
+            if (e < 0) continue;
+            Args b = a;
+            b.x = a.x + (size_t)s * a.ek;
+            b.k = a.ek;
+            b.k_pad = a.ekp;
+            const uint8_t* cbe[PW];
+            const uint8_t* ebe[PW];
+#pragma unroll
+            for (int q = 0; q < PW; ++q) {
+                cbe[q] = cb[q] + (size_t)e * a.cstride;
+                ebe[q] = eb[q] + (size_t)e * a.estride;
+            }
+            chunk(b, cbe, ebe, k0 - s * a.ekp, k1 - s * a.ekp);
         } else {
-            for (int b0 = k0 / 32; b0 < k1 / 32; b0 += 4) mgroup_bf16<MT, PW>(a, cb, b0, lane, acc);
+            chunk(a, cb, eb, k0, k1);
         }
     }
 #pragma unroll
@@ -937,7 +1162,11 @@ __global__ __launch_bounds__(512) void dr_mfma(const Args a) {
                 part[((wave * PW + q) * ROWS + 16 * tt + 4 * (lane >> 4) + j) * 16 + (lane & 15)] = acc[q][tt][j];
     __syncthreads();
     const int nparts = gather_splits<ROWS, PW>(a, g, split, part);
-    if (nparts) epilogue<ROWS, PW>(a, sg, t, part, nparts, tval, tkey, wave, lane);
+    if (!nparts) return;
+    if constexpr (moe_n<MOE>())
+        epilogue_moe<ROWS, MOE>(a, t, unit, ex, part, nparts);
+    else
+        epilogue<ROWS, PW>(a, sg, t, part, nparts, tval, tkey, wave, lane);
 }
 
 // ---- packing ---------------------------------------------------------------------------------------------------------
@@ -1167,14 +1396,18 @@ int hip_status(hipError_t e) { return e == hipSuccess ? DR_OK : DR_EHIP; }
 #define DR_SPLIT_CHUNKS 8
 #endif
 
-void plan(int k, int* chunks, int* kch, int* waves, int* splits, int* cps) {
-    const int k_pad = (k + KALIGN - 1) / KALIGN * KALIGN;
-    const int ch = DR_CHUNK_K ? DR_CHUNK_K : (k_pad >= 4096 ? 512 : 256);
+// the split of a padded K into chunks of ch
+void plan_chunks(int k_pad, int ch, int* chunks, int* kch, int* waves, int* splits, int* cps) {
     *kch = ch;
     *chunks = (k_pad + ch - 1) / ch;
     *splits = (*chunks + DR_SPLIT_CHUNKS - 1) / DR_SPLIT_CHUNKS;
     *cps = (*chunks + *splits - 1) / *splits;
     *waves = *cps < MAXW ? *cps : MAXW;
+}
+
+void plan(int k, int* chunks, int* kch, int* waves, int* splits, int* cps) {
+    const int k_pad = (k + KALIGN - 1) / KALIGN * KALIGN;
+    plan_chunks(k_pad, DR_CHUNK_K ? DR_CHUNK_K : (k_pad >= 4096 ? 512 : 256), chunks, kch, waves, splits, cps);
 }
 
 // the MFMA kernel from this many rows on; below it the GEMV kernel's rows a pass
@@ -1218,6 +1451,48 @@ void launch_mfma(const Args& a, int grid, hipStream_t st) {
         case DR_BFP4: hipLaunchKernelGGL((dr_mfma<MT, PW, DR_BFP4, true>), dim3(grid), b, lds, st, a); break;
         default: hipLaunchKernelGGL((dr_mfma<MT, PW, DR_BF16, true>), dim3(grid), b, lds, st, a); break;
     }
+}
+
+template <int MR, int PW, int MOE>
+void launch_gemv_moe(const Args& a, int grid, hipStream_t st) {
+    const dim3 b(64 * a.waves);
+    const size_t lds = (size_t)max(a.waves, a.splits) * PW * MR * 16 * sizeof(float);
+    hipLaunchKernelGGL((dr_gemv<MR, PW, DR_BFP4, true, MOE>), dim3(grid), b, lds, st, a);
+}
+
+template <int MT, int PW, int MOE>
+void launch_mfma_moe(const Args& a, int grid, hipStream_t st) {
+    const dim3 b(64 * a.waves);
+    const size_t lds = (size_t)max(a.waves, a.splits) * PW * 16 * MT * 16 * sizeof(float);
+    hipLaunchKernelGGL((dr_mfma<MT, PW, DR_BFP4, true, MOE>), dim3(grid), b, lds, st, a);
+}
+
+// one pass of an expert-gathered launch (bfloat4_b): the one-row modes on the GEMV; the rows modes on the GEMV up to
+// two rows, else the MFMA kernel (16 rows a pass for gate/up, 16 or 32 for down)
+hipError_t launch_moe(const Args& a, int mode, int rows, int grid, hipStream_t st) {
+    switch (mode) {
+        case DR_MOE_GATE_UP: launch_gemv_moe<1, 4, DR_MOE_GATE_UP>(a, grid, st); break;
+        case DR_MOE_DOWN: launch_gemv_moe<1, 2, DR_MOE_DOWN>(a, grid, st); break;
+        case DR_MOE_GATE_UP_ROWS:
+            if (rows == 1)
+                launch_gemv_moe<1, 4, DR_MOE_GATE_UP_ROWS>(a, grid, st);
+            else if (rows == 2)
+                launch_gemv_moe<2, 4, DR_MOE_GATE_UP_ROWS>(a, grid, st);
+            else
+                launch_mfma_moe<1, 4, DR_MOE_GATE_UP_ROWS>(a, grid, st);
+            break;
+        default:
+            if (rows == 1)
+                launch_gemv_moe<1, 2, DR_MOE_DOWN_ROWS>(a, grid, st);
+            else if (rows == 2)
+                launch_gemv_moe<2, 2, DR_MOE_DOWN_ROWS>(a, grid, st);
+            else if (rows == 16)
+                launch_mfma_moe<1, 2, DR_MOE_DOWN_ROWS>(a, grid, st);
+            else
+                launch_mfma_moe<2, 2, DR_MOE_DOWN_ROWS>(a, grid, st);
+            break;
+    }
+    return hipGetLastError();
 }
 
 // one pass of up to `rows` rows
@@ -1335,7 +1610,7 @@ int prepare(const dr_launch* L, Args& a, int& pw, int& tiles, int& mr) {
     a.ldr = L->ldr;
     a.res_mode = L->residual ? (L->residual_mode == 2 ? 2 : 1) : 0;
     a.act = L->act;
-    if (a.act != 0 && a.act != 1) return DR_EINVAL;
+    if (a.act < DR_ACT_SILU || a.act > DR_ACT_SWIGLU_OAI) return DR_EINVAL;
     a.nseg = L->nseg;
     pw = L->seg[0].glu ? 4 : 2;
     tiles = 0;
@@ -1476,5 +1751,111 @@ const char* dr_status_string(int s) {
 }
 
 int dr_version(void) { return 1; }
+
+}  // extern "C"
+
+// ---- the expert-gathered launches (include/moe.h) --------------------------------------------------------------------
+
+namespace {
+
+// the base launch's arguments (prepare), then the gather's: the tiles of the gate/up modes, the gathered K of the
+// down modes, the rows a pass
+int prepare_moe(const dr_launch* L, const dr_moe* M, Args& a, int& pw, int& tiles, int& mr) {
+    if (L == nullptr || M == nullptr || M->mode < DR_MOE_GATE_UP || M->mode > DR_MOE_DOWN_ROWS) return DR_EINVAL;
+    const int mode = M->mode;
+    const bool nmode = mode == DR_MOE_GATE_UP || mode == DR_MOE_GATE_UP_ROWS;
+    const bool rows = mode == DR_MOE_GATE_UP_ROWS || mode == DR_MOE_DOWN_ROWS;
+    if (M->ids == nullptr || M->slots < 1 || M->slots > 16 || M->ld_ids < M->slots || M->id_rows < 1 ||
+        M->id_rows > 32 || (!rows && M->id_rows != 1) || M->experts < 1 || (rows && M->experts > 1024) ||
+        M->codes_stride <= 0 || M->exps_stride <= 0)
+        return DR_EINVAL;
+    const dr_segment& s0 = L->seg[0];
+    if (L->nseg != 1 || L->residual != nullptr || L->topk.records != nullptr || s0.fmt != DR_BFP4 ||
+        s0.scale != nullptr || s0.scale_up != nullptr || s0.col0 != 0 || (s0.glu == 2) != nmode || (!nmode && s0.glu))
+        return DR_EINVAL;
+    if (L->m < 1 || L->m > (rows ? M->id_rows : 1)) return DR_EINVAL;
+    const int units = rows ? std::min(M->experts, M->id_rows * M->slots) : M->slots;
+    dr_launch B = *L;
+    int ekp = 0;
+    if (nmode) {
+        if (M->w == nullptr || M->ld_w < M->slots || M->expert_n != s0.n || L->y_f32 ||
+            (int64_t)L->ldy < (int64_t)units * M->expert_n)
+            return DR_EINVAL;
+    } else {
+        if (M->expert_k <= 0 || M->expert_k % 32 || L->k != units * M->expert_k) return DR_EINVAL;
+        ekp = (M->expert_k + KALIGN - 1) / KALIGN * KALIGN;
+        B.k = units * ekp;  // (the gathered K, each unit's block padded)
+        B.ldx = std::max(L->ldx, B.k);
+    }
+    const int st = prepare(&B, a, pw, tiles, mr);
+    if (st != DR_OK) return st;
+    a.ldx = L->ldx;
+    a.ids = M->ids;
+    a.ids32 = M->ids32 != 0;
+    a.ld_ids = M->ld_ids;
+    a.slots = M->slots;
+    a.id_rows = M->id_rows;
+    a.experts = M->experts;
+    a.rw = reinterpret_cast<const uint16_t*>(M->w);
+    a.ld_rw = M->ld_w;
+    a.cstride = M->codes_stride;
+    a.estride = M->exps_stride;
+    a.bias = reinterpret_cast<const uint16_t*>(M->bias);
+    if (nmode) {
+        a.en = M->expert_n;
+        a.tpe = (a.en + TILE - 1) / TILE;
+        tiles = units * a.tpe;
+        a.seg[0].tiles = tiles;
+        a.tiles = tiles;
+    } else {
+        a.ek = M->expert_k;
+        a.ekp = ekp;
+        a.seg[0].pstride = (unsigned)((ekp / kblk(DR_BFP4)) * 1024);
+        if (ekp % a.kch) plan_chunks(a.k_pad, 256, &a.chunks, &a.kch, &a.waves, &a.splits, &a.cps);  // (a chunk in one unit)
+    }
+    if (!rows)
+        mr = 1;
+    else if (L->m <= 2)
+        mr = L->m;
+    else
+        mr = (nmode || L->m <= 16) ? 16 : 32;
+    return DR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t dr_moe_workspace_bytes(const dr_launch* L, const dr_moe* M) {
+    Args a{};
+    int pw, tiles, mr;
+    if (prepare_moe(L, M, a, pw, tiles, mr) != DR_OK) return -1;
+    return workspace_bytes(a, pw, mr);
+}
+
+int dr_moe_matmul(const dr_launch* L, const dr_moe* M) {
+    Args a{};
+    int pw, tiles, mr;
+    const int st0 = prepare_moe(L, M, a, pw, tiles, mr);
+    if (st0 != DR_OK) return st0;
+    const int64_t need = workspace_bytes(a, pw, mr);
+    if (need > 0) {
+        if (L->workspace == nullptr || L->workspace_bytes < need) return DR_EINVAL;
+        a.counters = reinterpret_cast<uint32_t*>(L->workspace);
+        a.wpart = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(L->workspace) + (((int64_t)tiles * 4 + 255) / 256 * 256));
+    }
+    hipStream_t st = S(L->stream);
+    const size_t ysz = a.y_f32 ? 4 : 2;
+    for (int r0 = 0; r0 < L->m; r0 += mr) {
+        Args p = a;
+        p.m = L->m - r0 < mr ? L->m - r0 : mr;
+        p.x = a.x + (size_t)r0 * a.ldx;
+        p.y = reinterpret_cast<uint8_t*>(L->y) + (size_t)r0 * a.ldy * ysz;
+        p.row0 = r0;
+        const hipError_t e = launch_moe(p, M->mode, mr, tiles * a.splits, st);
+        if (e != hipSuccess) return DR_EHIP;
+    }
+    return DR_OK;
+}
 
 }  // extern "C"

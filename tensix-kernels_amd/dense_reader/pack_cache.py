@@ -57,11 +57,11 @@ def array_sums(arrays):
     return out
 
 
-def cache_read(path, meta, rebuild=False, verify=True):
-    """{name: array} from a cache made with the same meta (memory-mapped); None when there is none (no directory or an
-    empty one). A cache that differs from meta, cannot be read or (verify) does not match its sums raises
-    PackCacheMismatch and nothing is written; with rebuild it is None and the caller makes it again over it
-    (reference moe/moe8.py:289-321)."""
+def cache_read(path, meta, rebuild=False, verify=True, names=ARRAYS, what="dense_reader", hint=None):
+    """{name: array} of `names` from a cache made with the same meta (memory-mapped); None when there is none (no
+    directory or an empty one). A cache that differs from meta, cannot be read or (verify) does not match its sums
+    raises PackCacheMismatch and nothing is written; with rebuild it is None and the caller makes it again over it
+    (reference moe/moe8.py:289-321). hint(old meta, the keys that differ): a sentence for the message, or ""."""
     path = Path(path)
     if not path.exists() or (path.is_dir() and not any(path.iterdir())):
         return None
@@ -74,7 +74,7 @@ def cache_read(path, meta, rebuild=False, verify=True):
         old, why = None, "its meta.json is not a pack's"
     if old == meta:
         try:
-            arrays = {n: np.load(path / f"{n}.npy", mmap_mode="r") for n in ARRAYS if (path / f"{n}.npy").exists()}
+            arrays = {n: np.load(path / f"{n}.npy", mmap_mode="r") for n in names if (path / f"{n}.npy").exists()}
             if verify:
                 sums = json.loads((path / "sums.json").read_text())
                 got = array_sums(arrays)
@@ -84,14 +84,16 @@ def cache_read(path, meta, rebuild=False, verify=True):
             return arrays
         except (OSError, ValueError) as e:
             why = f"its arrays cannot be read or are damaged ({type(e).__name__}: {e})"
-    elif old is not None:
+    extra = ""
+    if old is not None and old != meta:
         keys = sorted(set(old) | set(meta), key=str)
         diff = [k for k in keys if old.get(k) != meta.get(k)]
         why = "; ".join(f"{k}: cache {_short(old.get(k))}, call {_short(meta.get(k))}" for k in diff)
+        extra = hint(old, diff) if hint is not None else ""
     if rebuild:
         return None
     raise PackCacheMismatch(
-        f"dense_reader pack cache {path} does not match this call ({why}). It was neither taken nor overwritten. "
+        f"{what} pack cache {path} does not match this call ({why}). It was neither taken nor overwritten.{extra} "
         "To pack again from these weights over it, pass rebuild=True."
     )
 

@@ -1,6 +1,6 @@
 """Benchmark of the dense_reader decode matmul on one MI355X.
 
-  python bench.py [--steps K] [--warmup W] [--config ns|c1|c2|c3|c4|c5|int4|lm] [--no-cpu] [--cpu-seconds S]
+  python bench.py [--steps K] [--warmup W] [--config ns|c1|c2|c3|c4|c5|int4|moe|lm] [--no-cpu] [--cpu-seconds S]
   python bench.py --copy-probe      (a plain 256 MiB copy kernel: the byte counters' calibration under rocprofv3)
 
 Default workload: the north-star decode matmul, bfloat8_b M=1, x [1, 4096] bf16 @ W [4096 in, 14336 out] (W ~
@@ -71,6 +71,14 @@ CONFIGS = {
         [(14336, "int4", True)],
         {"int4": True},
     ),
+    "moe": (
+        "MoE layer decode, gpt-oss-20b shape: E=32 experts, top-4, H=2880, I=2880, swiglu_oai with gate/up bias, "
+        "bfp4 experts; a step is route (softmax top-4 of the router logits) + gate_up + down (moe8)",
+        1,
+        2880,
+        [(2880, "bfp4", False)],
+        {"moe": (32, 4, 2880, 2880)},
+    ),
     "lm": (
         "LM head to token ids, M=4 K=4096 vocab=128256 bfp8: bf16 top-8 records, the best 16 rescored from the bf16 "
         "rows and picked on the device (lm_head_topk DeviceHead, device_pick)",
@@ -134,6 +142,10 @@ class Workload:
         self.x = torch.randn(m, k, generator=g, device="cuda").to(torch.bfloat16).reshape(1, 1, m, k)
 
         self.heads = None
+        self.kbytes = None  # bytes of the dominant kernel a launch (default: the step's weight bytes)
+        if o.get("moe"):
+            self._init_moe(dev, g, torch)
+            return
         if o.get("int4"):
             from int4 import w4a16
 
@@ -184,7 +196,48 @@ class Workload:
             self.col0.append(c // 32)
             c += nb
 
+    def _init_moe(self, dev, g, torch):
+        """The MoE layer: E experts packed once (their fp32 weights made on the GPU and dropped), E / k disjoint sets
+        of k experts that steps cycle through (each set's router logits favour it; the ids and weights of each set are
+        routed once for the kernel-alone timing), and one token x."""
+        from moe import moe8
+
+        E, k, H, I = self.o["moe"]
+        self.moe8, self.moe_shape = moe8, (E, k, H, I)
+        gate_up = torch.randn(E, H, 2 * I, generator=g, device="cuda") * 0.02
+        down = torch.randn(E, I, H, generator=g, device="cuda") * 0.02
+        bias = torch.randn(E, 2 * I, generator=g, device="cuda") * 0.1
+        self.P = moe8.pack(dev, gate_up, down, gu_bias=bias)
+        self.host_w = (gate_up[:k].cpu(), down[:k].cpu(), bias[:k].cpu())  # (the CPU baseline's experts)
+        del gate_up, down
+        nsets = E // k
+        self.logits = []
+        for s_ in range(nsets):
+            lg = torch.randn(1, 1, 1, E, generator=g, device="cuda") * 0.5
+            lg[..., s_ * k : (s_ + 1) * k] += 10.0
+            self.logits.append(lg)
+        self.ids = torch.zeros(1, 1, 1, k, dtype=torch.int16, device="cuda")
+        self.wts = torch.zeros(1, 1, 1, k, dtype=torch.bfloat16, device="cuda")
+        self.set_ids, self.set_wts = [], []
+        for lg in self.logits:
+            ti = torch.zeros(1, 1, 1, k, dtype=torch.int16, device="cuda")
+            tw = torch.zeros(1, 1, 1, k, dtype=torch.bfloat16, device="cuda")
+            moe8.route(lg, ti, tw, k)
+            self.set_ids.append(ti)
+            self.set_wts.append(tw)
+        self.x = (torch.randn(1, 1, 1, H, generator=g, device="cuda")).to(torch.bfloat16)
+        tile = 576  # the reference's bytes of a BFP4_b tile
+        self.kbytes = k * (H // 32) * (2 * I // 32) * tile  # gate_up
+        self.wbytes = self.kbytes + k * (I // 32) * (H // 32) * tile  # + down
+        self.copies = nsets
+        self.scales, self.res, self.rec, self.n = [None], None, None, H
+
     def kernel(self, i):
+        if self.o.get("moe"):
+            _, k, _, _ = self.moe_shape
+            s_ = i % self.copies
+            self.moe8.gate_up(self.x, self.P, self.set_ids[s_], self.set_wts[s_], k, act="swiglu_oai")
+            return
         L, o, ws = self.linear, self.o, self.sets[i % self.copies]
         if o.get("glu2"):
             L.matmul(self.x, ws[0], self.scales[0], out=self.y, glu=True, w_up=ws[1], scale_up=self.scales[1])
@@ -208,6 +261,12 @@ class Workload:
             L.matmul(self.x, ws[0], None, out=self.y)
 
     def step(self, i):
+        if self.o.get("moe"):
+            m8, (_, k, _, _) = self.moe8, self.moe_shape
+            m8.route(self.logits[i % self.copies], self.ids, self.wts, k)
+            h = m8.gate_up(self.x, self.P, self.ids, self.wts, k, act="swiglu_oai")
+            m8.down(h, self.P, self.ids, k)
+            return
         if self.o.get("lmhead"):
             self.heads[i % self.copies].logits_topk(self.x, self.m)
             return
@@ -285,9 +344,11 @@ def main():
     total_ms = timed_graph(torch, wl.step, a.steps)
     ms_per_step = total_ms / a.steps
     value = wl.wbytes * a.steps / (total_ms * 1e-3) / 1e9
-    kern_ms = total_ms if not (wl.o.get("topk") or wl.o.get("lmhead")) else timed_graph(torch, wl.kernel, a.steps)
+    several = wl.o.get("topk") or wl.o.get("lmhead") or wl.o.get("moe")  # (steps of more than the one launch)
+    kern_ms = timed_graph(torch, wl.kernel, a.steps) if several else total_ms
     launch_us = kern_ms * 1e3 / a.steps
-    achieved = wl.wbytes / (launch_us * 1e-6) / 1e9
+    kbytes = wl.kbytes or wl.wbytes
+    achieved = kbytes / (launch_us * 1e-6) / 1e9
 
     cpu = None if a.no_cpu else cpu_baseline(wl, a.cpu_seconds)
     fmts = sorted({f for _, f, _ in wl.spec})
@@ -314,6 +375,9 @@ def main():
             "n": [n for n, _, _ in wl.spec],
             "weight_bytes_per_call": wl.wbytes,
             "weight_copies_rotated": wl.copies,
+            **({"experts": wl.moe_shape[0], "top_k": wl.moe_shape[1], "hidden": wl.moe_shape[2],
+                "intermediate": wl.moe_shape[3], "kernel": "gate_up (the step's larger launch)"}
+               if wl.o.get("moe") else {}),
             "timing": "HIP graph of the timed steps, replayed; events on the replay stream",
         },
         "eager_us_per_call": {"median": round(eager[len(eager) // 2], 3), "min": round(eager[0], 3)},
@@ -325,7 +389,7 @@ def main():
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic_row(a.config),
             "launch_us": round(launch_us, 3),
-            "algorithmic_bytes": wl.wbytes,
+            "algorithmic_bytes": kbytes,
         },
         "cpu_baseline": cpu,
     }
@@ -343,6 +407,20 @@ def cpu_baseline(wl, seconds):
     torch.set_num_threads(threads)
     m, o = wl.m, wl.o
     xc = wl.x.reshape(m, -1).cpu()
+    if o.get("moe"):  # the reference's host check of the layer (moe8.py:642-660), float32, the k experts of a step
+        gu, dn, bias = wl.host_w
+        E, k, H, I = wl.moe_shape
+        xm = wl.x.reshape(1, H).cpu().float()
+        wr = torch.full((k,), 1.0 / k)
+
+        def moe_step():
+            pre = torch.stack([xm[0] @ gu[e] for e in range(k)]) + bias.to(torch.bfloat16).float()
+            gc = pre[:, I:].clamp(max=7.0)
+            h = gc * torch.sigmoid(1.702 * gc) * (pre[:, :I].clamp(-7.0, 7.0) + 1.0) * wr[:, None]
+            return sum(h[e] @ dn[e] for e in range(k))
+
+        return _time_cpu(wl, moe_step, seconds, threads, "a float32 port of the reference's layer check (the k "
+                         "experts' gate_up, the clamped SwiGLU, the routing weights and down)")
     if o.get("int4"):  # the reference's host check: x (bf16) @ (q * s).T in float32 (int4/w4a16.py:100-107)
         hw = [O.int4_dequantized(w.codes.cpu(), w.scales.cpu()).float().T.contiguous() for w in wl.sets[0]]
     else:
@@ -364,6 +442,12 @@ def cpu_baseline(wl, seconds):
             torch.topk(y, 32 if o.get("topk") else 16, dim=1)
         return y
 
+    return _time_cpu(wl, step, seconds, threads, "oracle.ref_f32 (x bf16->f32 @ held W f32; int4: W = q * s) plus the "
+                     "epilogue")
+
+
+def _time_cpu(wl, step, seconds, threads, what):
+    """The median time of step() over about `seconds` (two untimed calls first), as the bench's cpu_baseline."""
     for _ in range(2):
         step()
     times = []
@@ -380,9 +464,7 @@ def cpu_baseline(wl, seconds):
         "us_per_call": round(med * 1e6, 1),
         "cores": threads,
         "kind": "port",
-        "sample": f"{len(times)} calls (median) of oracle.ref_f32 (x bf16->f32 @ held W f32; int4: W = q * s) plus "
-        "the epilogue, "
-        f"the full config shapes, {threads} threads, ~{seconds:.0f} s",
+        "sample": f"{len(times)} calls (median) of {what}, the full config shapes, {threads} threads, ~{seconds:.0f} s",
     }
 
 

@@ -8,13 +8,13 @@
  *   down:    expert e's weight [K = I, N = H] at codes + e * codes_stride.
  *
  * Reference interfaces replaced (XylolabsInc/tensix-kernels, paths relative to its root):
- *   dr_moe_matmul, mode DR_MOE_GATE_UP       <- moe/moe8.py:710-815 gate_up and its kernels moe_gu_reader.cpp,
+ *   dr_moe_matmul, mode DR_MOE_GATE_UP       <- moe/moe8.py:710-817 gate_up and its kernels moe_gu_reader.cpp,
  *                                               moe_gu2_reader.cpp, moe_gu_compute.cpp, moe_gu_writer.cpp
- *   dr_moe_matmul, mode DR_MOE_DOWN          <- moe/moe8.py:818-900 down and moe_dn_*.cpp, moe_dn2_*.cpp
- *   dr_moe_matmul, mode DR_MOE_GATE_UP_ROWS  <- moe/moe8.py:925-1036 gate_up_rows and moe_gur_*.cpp, moe8_rows.h
- *   dr_moe_matmul, mode DR_MOE_DOWN_ROWS     <- moe/moe8.py:1039-1139 down_rows and moe_dnr_*.cpp
+ *   dr_moe_matmul, mode DR_MOE_DOWN          <- moe/moe8.py:820-910 down and moe_dn_*.cpp, moe_dn2_*.cpp
+ *   dr_moe_matmul, mode DR_MOE_GATE_UP_ROWS  <- moe/moe8.py:928-1037 gate_up_rows and moe_gur_*.cpp, moe8_rows.h
+ *   dr_moe_matmul, mode DR_MOE_DOWN_ROWS     <- moe/moe8.py:1040-1136 down_rows and moe_dnr_*.cpp
  *   dr_moe_workspace_bytes                   <- (no counterpart: split K meets in caller memory, as dr_workspace_bytes)
- *   dr_moe_route                             <- moe/moe8.py:1145-1257 route and moe_route.cpp
+ *   dr_moe_route                             <- moe/moe8.py:1139-1253 route and moe_route.cpp
  */
 #ifndef DR_MOE_H
 #define DR_MOE_H

@@ -6,12 +6,12 @@ checker; the product (tensix-kernels_amd/) never does.
 It restates, in numpy float64 on the CPU, what XylolabsInc/tensix-kernels' moe/moe8.py computes (paths relative to the
 reference's root):
 
-- glu: the experts' activation times the up half, moe8.py:629-639 and moe_gu_compute.cpp (silu, gelu_tanh as
+- glu: the experts' activation times the up half, moe8.py:607-616 and moe_gu_compute.cpp (silu, gelu_tanh as
   HF's gelu_pytorch_tanh, swiglu_oai as gpt-oss's clamped SwiGLU, common/kernels/dense_ops.h:90-118);
-- layer / layer_rows: one row's h and y (moe8.py:642-669): per slot s, w_s * glu(x G_e + b_g, x U_e + b_u), gate_up
+- layer / layer_rows: one row's h and y (moe8.py:619-644): per slot s, w_s * glu(x G_e + b_g, x U_e + b_u), gate_up
   [E, H, 2I] as [up | gate] columns, then y = sum_s h_s @ D_e;
-- union: the rows' distinct ids below E in increasing order (moe8.py:672-674, kernels/moe8_rows.h);
-- route: the router, one row at a time in plain Python (moe8.py:1145-1286): keys, optional group-limited routing,
+- union: the rows' distinct ids below E in increasing order (moe8.py:647-649, kernels/moe8_rows.h);
+- route: the router, one row at a time in plain Python (moe8.py:1139-1286): keys, optional group-limited routing,
   the top k by key with the lower id first among equal keys, the softmax or sigmoid weights, the scale, a fixed slot.
 
 What pins each function (tests/test_oracle.py, test_moe_oracle_*):
@@ -39,7 +39,7 @@ def _sigmoid(z):
 
 def glu(g, u, act):
     """act(g) * u in float64 (numpy arrays): silu g * sigmoid(g); gelu_tanh 0.5 g (1 + tanh(sqrt(2 / pi) (g +
-    0.044715 g^3))); swiglu_oai min(g, 7) * sigmoid(1.702 min(g, 7)) * (clip(u, -7, 7) + 1) (moe8.py:629-639)."""
+    0.044715 g^3))); swiglu_oai min(g, 7) * sigmoid(1.702 min(g, 7)) * (clip(u, -7, 7) + 1) (moe8.py:607-616)."""
     g, u = np.asarray(g, np.float64), np.asarray(u, np.float64)
     if act == "silu":
         return g * _sigmoid(g) * u
@@ -61,7 +61,7 @@ def _bf16(a):
 def layer(x, gate_up, down, ids, w, act="silu", gu_bias=None):
     """(y [H], h [k * I]) in float64 for one row x [H]: slot s of h = w[s] * glu(x G_e + b_g, x U_e + b_u) with e =
     ids[s], G_e = gate_up[e][:, I:], U_e = gate_up[e][:, :I], b = gu_bias[e] rounded to bf16 ([up | gate]); y = the
-    sum over the slots of h_s @ down[e] (moe8.py:642-660)."""
+    sum over the slots of h_s @ down[e] (moe8.py:619-636)."""
     x = np.asarray(x, np.float64).reshape(-1)
     gu = np.asarray(gate_up, np.float64)
     dn = np.asarray(down, np.float64)

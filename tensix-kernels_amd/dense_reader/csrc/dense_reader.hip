@@ -98,7 +98,12 @@ struct Args {
     int splits, cps, tiles;  // split K: splits workgroups a tile, cps chunks each; tiles of the launch
     uint32_t* counters;      // [tiles] (splits > 1): workgroups of the tile done, reset to 0 by the last
     float* wpart;            // [tiles][splits][PW * ROWS * 16] (splits > 1): each workgroup's column sums
-    // expert gather (DR_MOE_*): the workgroup's expert (gate/up modes) or each chunk's (down modes), read from ids
+};
+
+// the expert-gathered launches' arguments (DR_MOE_*): the workgroup's expert (gate/up modes) or each chunk's (down
+// modes), read from ids. A struct of their own: the dense kernels keep Args as it is (a larger argument block moved
+// the compiler's register choices in the dense K loop).
+struct MoeArgs : Args {
     const void* ids;
     int ids32, ld_ids, slots, id_rows, experts;
     const uint16_t* rw;  // routing weights [id_rows][ld_rw] bf16
@@ -422,17 +427,23 @@ __device__ __forceinline__ float load_scale(const void* s, int f32, int col) {
     return f32 ? reinterpret_cast<const float*>(s)[col] : bf16_to_f32(reinterpret_cast<const uint16_t*>(s)[col]);
 }
 
-// act(g) * u: silu(g) = g * sigmoid(g); gelu_tanh(g) = g * sigmoid(1.5957691216 g + 0.0713548162 g^3)
-// (dense_ops.h:46-59); swiglu_oai min(g, 7) * sigmoid(1.702 min(g, 7)) * (clamp(u, -7, 7) + 1) (dense_ops.h:90-118),
-// a NaN passing through the clamps as it does there
+// the dense GLU's activation: silu(g) = g * sigmoid(g); gelu_tanh(g) = g * sigmoid(1.5957691216 g + 0.0713548162 g^3)
+// (dense_ops.h:46-59)
+__device__ __forceinline__ float act_glu(float g, int act) {
+    const float z = act == DR_ACT_GELU_TANH ? g * (1.5957691216f + 0.0713548162f * (g * g)) : g;
+    return g / (1.f + __expf(-z));
+}
+
+// the experts' act(g) * u: act_glu's two, or swiglu_oai min(g, 7) * sigmoid(1.702 min(g, 7)) * (clamp(u, -7, 7) + 1)
+// (dense_ops.h:90-118), a NaN passing through the clamps as it does there (the dense GLU keeps act_glu alone: the
+// third branch in its epilogue costs the dense K loop registers)
 __device__ __forceinline__ float glu(float g, float u, int act) {
     if (act == DR_ACT_SWIGLU_OAI) {
         const float gc = g > 7.f ? 7.f : g;
         const float uc = u > 7.f ? 7.f : (u < -7.f ? -7.f : u);
         return gc / (1.f + __expf(-(1.702f * gc))) * (uc + 1.f);
     }
-    const float z = act == DR_ACT_GELU_TANH ? g * (1.5957691216f + 0.0713548162f * (g * g)) : g;
-    return g / (1.f + __expf(-z)) * u;
+    return act_glu(g, act) * u;
 }
 
 // the reference's top-k key of a bf16 (dense_writer.cpp:215): a monotonic uint16, 0 below everything
@@ -445,7 +456,7 @@ __device__ __forceinline__ uint32_t key_f32(float f) {
 // ---- expert gather: ids, the union of the rows' ids ----------------------------------------------------------------
 
 // expert id j of row r, or -1 when it is not below the expert count (it chooses nothing)
-__device__ __forceinline__ int moe_id(const Args& a, int r, int j) {
+__device__ __forceinline__ int moe_id(const MoeArgs& a, int r, int j) {
     const size_t i = (size_t)r * a.ld_ids + j;
     const uint32_t e = a.ids32 ? reinterpret_cast<const uint32_t*>(a.ids)[i] : reinterpret_cast<const uint16_t*>(a.ids)[i];
     return e < (uint32_t)a.experts ? (int)e : -1;
@@ -465,7 +476,7 @@ __device__ __forceinline__ UnionLds* union_lds() {
 }
 
 // every thread of the workgroup calls it: a bitmap of the ids, then wavefront 0 lists its set bits in order
-__device__ __forceinline__ void moe_union(const Args& a, UnionLds& u) {
+__device__ __forceinline__ void moe_union(const MoeArgs& a, UnionLds& u) {
     for (int i = threadIdx.x; i < 32; i += blockDim.x) u.bits[i] = 0u;
     __syncthreads();
     for (int i = threadIdx.x; i < a.id_rows * a.slots; i += blockDim.x) {
@@ -561,7 +572,7 @@ __device__ __forceinline__ void epilogue(const Args& a, const SegDev& sg, int t,
                     suv = load_scale(sg.scale_up, sg.scale_f32, oc);
                 }
             }
-            v = glu(gsum * sgv, usum * suv, a.act);
+            v = act_glu(gsum * sgv, a.act) * (usum * suv);
         } else {
             const size_t ycol = (size_t)sg.col0 + oc;
             if (valid && a.res != nullptr && a.res_mode == 2) v = bf16_to_f32(a.res[(size_t)m * a.ldr + ycol]);
@@ -625,7 +636,7 @@ __device__ __forceinline__ void epilogue(const Args& a, const SegDev& sg, int t,
 // for the expert (the slot's in DR_MOE_GATE_UP; 0 where the row did not choose it in DR_MOE_GATE_UP_ROWS) and writes
 // the unit's columns of y (moe_gu_compute.cpp: the GLU in dest, then times the weight's tile)
 template <int ROWS, int MOE>
-__device__ __forceinline__ void epilogue_moe(const Args& a, int t, int unit, int ex, const float* part, int nparts) {
+__device__ __forceinline__ void epilogue_moe(const MoeArgs& a, int t, int unit, int ex, const float* part, int nparts) {
     constexpr int PW = 4;
     __shared__ float coef[ROWS];
     const int mrows = min(a.m, ROWS);
@@ -663,7 +674,7 @@ __device__ __forceinline__ void epilogue_moe(const Args& a, int t, int unit, int
 }
 
 // DR_MOE_GATE_UP with an id past the experts: the slot's columns of this tile are zeros
-__device__ __forceinline__ void moe_zero(const Args& a, int t, int unit) {
+__device__ __forceinline__ void moe_zero(const MoeArgs& a, int t, int unit) {
     for (int col = threadIdx.x; col < TILE; col += blockDim.x) {
         const int oc = t * TILE + col;
         if (oc < a.en) reinterpret_cast<uint16_t*>(a.y)[(size_t)unit * a.en + oc] = 0;
@@ -717,13 +728,7 @@ __device__ __forceinline__ int gather_splits(const Args& a, int g, int split, fl
 // ---- the GEMV kernel (few rows): VALU decode and FMA, one accumulator a lane per panel and row -----------------------
 //
 // FMT >= 0: every segment has that format (one K loop compiled in: a smaller kernel); FMT < 0: each workgroup
-// branches on its segment's format. ONE: a single segment. MOE: an expert gather (DR_MOE_*, bfloat4_b, one segment)
-// or 0.
-//
-// The expert gather. Gate/up modes: the launch's tiles are units (slots, or the union's experts) times the expert's
-// tiles; the workgroup's unit gives its expert, whose weights sit cstride / estride bytes per expert further on.
-// Down modes: the launch's K is the units' blocks of ekp rows one after another; a chunk lies in one unit (ekp is a
-// multiple of the chunk), whose expert gives that chunk's weights and whose ek values of x sit at unit * ek.
+// branches on its segment's format. ONE: a single segment.
 template <int MOE>
 __device__ __forceinline__ constexpr bool moe_k() {
     return MOE == DR_MOE_DOWN || MOE == DR_MOE_DOWN_ROWS;
@@ -733,7 +738,7 @@ __device__ __forceinline__ constexpr bool moe_n() {
     return MOE == DR_MOE_GATE_UP || MOE == DR_MOE_GATE_UP_ROWS;
 }
 
-template <int MR, int PW, int FMT, bool ONE, int MOE = 0>
+template <int MR, int PW, int FMT, bool ONE>
 __global__ __launch_bounds__(512) void dr_gemv(const Args a) {
     extern __shared__ float part[];  // [W][PW][MR][16]
     __shared__ float tval[MR][TILE];
@@ -741,11 +746,96 @@ __global__ __launch_bounds__(512) void dr_gemv(const Args a) {
 
     const int g = blockIdx.x % a.tiles, split = blockIdx.x / a.tiles;
     const SegDev& sg = a.seg[find_segment<ONE>(a, g)];
-    int t = g - sg.tile_begin;
+    const int t = g - sg.tile_begin;
     // (the wavefront index is uniform across the wavefront; readfirstlane lets the compiler see it, so the chunk
     // bounds and loop trip counts live in SGPRs and the K loops branch on scalars)
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int fmt = FMT >= 0 ? FMT : sg.fmt;
+    const uint8_t* cb[PW];
+    const uint8_t* eb[PW];
+    panel_ptrs<PW>(sg, t, a.k_pad, cb, eb);
+
+    float wsum[PW][MR];  // this wavefront's column sums (lanes 0..15), its chunks added in order
+#pragma unroll
+    for (int q = 0; q < PW; ++q)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) wsum[q][m] = 0.f;
+    const int ch1 = min((split + 1) * a.cps, a.chunks);
+    for (int ch = split * a.cps + wave; ch < ch1; ch += a.waves) {
+        float acc[PW][MR], corr[PW][MR];
+#pragma unroll
+        for (int q = 0; q < PW; ++q)
+#pragma unroll
+            for (int m = 0; m < MR; ++m) acc[q][m] = corr[q][m] = 0.f;
+        const int k0 = ch * a.kch, k1 = min(k0 + a.kch, a.k_pad);
+        if (fmt == DR_BFP8) {
+            chunk_bfp8<MR, PW>(a, cb, eb, k0, k1, lane, acc);
+        } else if (FMT == DR_INT4) {
+            const uint16_t* gs[PW];
+#pragma unroll
+            for (int q = 0; q < PW; ++q) gs[q] = sg.gscale + (size_t)(2 * t + q) * (a.k_pad / 128) * 64;
+            chunk_int4<MR, PW>(a, cb, gs, k0, k1, lane, acc);
+        } else if (fmt == DR_BFP4) {
+            float sx[PW][MR];
+#pragma unroll
+            for (int q = 0; q < PW; ++q)
+#pragma unroll
+                for (int m = 0; m < MR; ++m) sx[q][m] = 0.f;
+            chunk_bfp4<MR, PW>(a, cb, eb, k0, k1, lane, acc, sx);
+            // the wavefront's 136 * sum x' (every lane made distinct x'), taken off every column
+#pragma unroll
+            for (int q = 0; q < PW; ++q)
+#pragma unroll
+                for (int m = 0; m < MR; ++m) {
+                    float v = sx[q][m];
+#pragma unroll
+                    for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o);
+                    corr[q][m] = 136.f * v;
+                }
+        } else {
+            chunk_bf16<MR, PW>(a, cb, k0, k1, lane, acc);
+        }
+        // the chunk's column sums: the four quarter-rows of each column, in a fixed order
+#pragma unroll
+        for (int q = 0; q < PW; ++q)
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                float v = acc[q][m];
+                v += __shfl_xor(v, 16);
+                v += __shfl_xor(v, 32);
+                wsum[q][m] += v - corr[q][m];
+            }
+    }
+    if (lane < 16) {
+#pragma unroll
+        for (int q = 0; q < PW; ++q)
+#pragma unroll
+            for (int m = 0; m < MR; ++m) part[((wave * PW + q) * MR + m) * 16 + lane] = wsum[q][m];
+    }
+    __syncthreads();
+    const int nparts = gather_splits<MR, PW>(a, g, split, part);
+    if (nparts) epilogue<MR, PW>(a, sg, t, part, nparts, tval, tkey, wave, lane);
+}
+
+
+// ---- the expert gather (include/moe.h): the GEMV and MFMA kernels over the chosen experts' bfloat4_b weights ----------
+//
+// Kernels of their own (the dense kernels stay as they are: a gather branch in them, even compiled out, moved the
+// compiler's scheduling of the dense K loop). Gate/up modes: the launch's tiles are units (slots, or the union's
+// experts) times the expert's tiles; the workgroup's unit gives its expert, whose weights sit cstride / estride bytes
+// per expert further on. Down modes: the launch's K is the units' blocks of ekp rows one after another; a chunk lies in
+// one unit (ekp is a multiple of the chunk), whose expert gives that chunk's weights and whose ek values of x sit at
+// unit * ek.
+template <int MR, int PW, int MOE>
+__global__ __launch_bounds__(512) void dr_gemv_moe(const MoeArgs a) {
+    extern __shared__ float part[];  // [W][PW][MR][16]
+    __shared__ float tval[MR][TILE];
+    __shared__ uint32_t tkey[MR][TILE];
+
+    const int g = blockIdx.x % a.tiles, split = blockIdx.x / a.tiles;
+    const SegDev& sg = a.seg[0];
+    int t = g - sg.tile_begin;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     UnionLds* ul = nullptr;
     if constexpr (MOE == DR_MOE_GATE_UP_ROWS || MOE == DR_MOE_DOWN_ROWS) {
         ul = union_lds<MOE>();
@@ -780,47 +870,24 @@ __global__ __launch_bounds__(512) void dr_gemv(const Args a) {
         for (int m = 0; m < MR; ++m) wsum[q][m] = 0.f;
     // one chunk [k0, k1) of x (b) against the panels cbx / ebx, added to wsum
     auto chunk = [&](const Args& b, const uint8_t* const* cbx, const uint8_t* const* ebx, int k0, int k1) {
-        float acc[PW][MR], corr[PW][MR];
+        float acc[PW][MR], sx[PW][MR];
 #pragma unroll
         for (int q = 0; q < PW; ++q)
 #pragma unroll
-            for (int m = 0; m < MR; ++m) acc[q][m] = corr[q][m] = 0.f;
-        if (fmt == DR_BFP8) {
-            chunk_bfp8<MR, PW>(b, cbx, ebx, k0, k1, lane, acc);
-        } else if (FMT == DR_INT4) {
-            const uint16_t* gs[PW];
-#pragma unroll
-            for (int q = 0; q < PW; ++q) gs[q] = sg.gscale + (size_t)(2 * t + q) * (b.k_pad / 128) * 64;
-            chunk_int4<MR, PW>(b, cbx, gs, k0, k1, lane, acc);
-        } else if (fmt == DR_BFP4) {
-            float sx[PW][MR];
-#pragma unroll
-            for (int q = 0; q < PW; ++q)
-#pragma unroll
-                for (int m = 0; m < MR; ++m) sx[q][m] = 0.f;
-            chunk_bfp4<MR, PW>(b, cbx, ebx, k0, k1, lane, acc, sx);
-            // the wavefront's 136 * sum x' (every lane made distinct x'), taken off every column
-#pragma unroll
-            for (int q = 0; q < PW; ++q)
-#pragma unroll
-                for (int m = 0; m < MR; ++m) {
-                    float v = sx[q][m];
-#pragma unroll
-                    for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o);
-                    corr[q][m] = 136.f * v;
-                }
-        } else {
-            chunk_bf16<MR, PW>(b, cbx, k0, k1, lane, acc);
-        }
-        // the chunk's column sums: the four quarter-rows of each column, in a fixed order
+            for (int m = 0; m < MR; ++m) acc[q][m] = sx[q][m] = 0.f;
+        chunk_bfp4<MR, PW>(b, cbx, ebx, k0, k1, lane, acc, sx);
+        // the chunk's column sums less the wavefront's 136 * sum x', as dr_gemv's
 #pragma unroll
         for (int q = 0; q < PW; ++q)
 #pragma unroll
             for (int m = 0; m < MR; ++m) {
+                float c = sx[q][m];
+#pragma unroll
+                for (int o = 1; o < 64; o <<= 1) c += __shfl_xor(c, o);
                 float v = acc[q][m];
                 v += __shfl_xor(v, 16);
                 v += __shfl_xor(v, 32);
-                wsum[q][m] += v - corr[q][m];
+                wsum[q][m] += v - 136.f * c;
             }
     };
     const int ch1 = min((split + 1) * a.cps, a.chunks);
@@ -831,7 +898,7 @@ __global__ __launch_bounds__(512) void dr_gemv(const Args a) {
             int e = MOE == DR_MOE_DOWN ? moe_id(a, 0, s) : (s < ul->count ? (int)ul->list[s] : -1);
             e = __builtin_amdgcn_readfirstlane(e);
             if (e < 0) continue;  // (an id past the experts, or a block past the union: nothing to add)
-            Args b = a;
+            Args b = a;  // (the chunk's view of x: the unit's block)
             b.x = a.x + (size_t)s * a.ek;
             b.k = a.ek;
             b.k_pad = a.ekp;
@@ -1075,7 +1142,7 @@ __device__ __forceinline__ void mgroup_bf16(const Args& a, const uint8_t* const*
             for (int tt = 0; tt < MT; ++tt) acc[q][tt] = mfma(A[u][tt], c[u][q], acc[q][tt]);
 }
 
-template <int MT, int PW, int FMT, bool ONE, int MOE = 0>
+template <int MT, int PW, int FMT, bool ONE>
 __global__ __launch_bounds__(512) void dr_mfma(const Args a) {
     constexpr int ROWS = 16 * MT;
     extern __shared__ float part[];  // [W][PW][ROWS][16]
@@ -1084,10 +1151,53 @@ __global__ __launch_bounds__(512) void dr_mfma(const Args a) {
 
     const int g = blockIdx.x % a.tiles, split = blockIdx.x / a.tiles;
     const SegDev& sg = a.seg[find_segment<ONE>(a, g)];
-    int t = g - sg.tile_begin;
+    const int t = g - sg.tile_begin;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int fmt = FMT >= 0 ? FMT : sg.fmt;
-    // the expert gather, as dr_gemv's (only the rows modes take more than two rows)
+    const uint8_t* cb[PW];
+    const uint8_t* eb[PW];
+    panel_ptrs<PW>(sg, t, a.k_pad, cb, eb);
+
+    f32x4 acc[PW][MT];  // this wavefront's sums over its chunks, in order
+#pragma unroll
+    for (int q = 0; q < PW; ++q)
+#pragma unroll
+        for (int tt = 0; tt < MT; ++tt) acc[q][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int ch1 = min((split + 1) * a.cps, a.chunks);
+    for (int ch = split * a.cps + wave; ch < ch1; ch += a.waves) {
+        const int k0 = ch * a.kch, k1 = min(k0 + a.kch, a.k_pad);
+        if (fmt == DR_BFP8) {
+            for (int gg = k0 >> 8; gg < (k1 >> 8); ++gg) mgroup_bfp8<MT, PW>(a, cb, eb, gg, lane, acc);
+        } else if (fmt == DR_BFP4) {
+            for (int gg = k0 >> 8; gg < (k1 >> 8); ++gg) mgroup_bfp4<MT, PW>(a, cb, eb, gg, lane, acc);
+        } else {
+            for (int b0 = k0 / 32; b0 < k1 / 32; b0 += 4) mgroup_bf16<MT, PW>(a, cb, b0, lane, acc);
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < PW; ++q)
+#pragma unroll
+        for (int tt = 0; tt < MT; ++tt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                part[((wave * PW + q) * ROWS + 16 * tt + 4 * (lane >> 4) + j) * 16 + (lane & 15)] = acc[q][tt][j];
+    __syncthreads();
+    const int nparts = gather_splits<ROWS, PW>(a, g, split, part);
+    if (nparts) epilogue<ROWS, PW>(a, sg, t, part, nparts, tval, tkey, wave, lane);
+}
+
+template <int MT, int PW, int MOE>
+__global__ __launch_bounds__(512) void dr_mfma_moe(const MoeArgs a) {
+    constexpr int ROWS = 16 * MT;
+    extern __shared__ float part[];  // [W][PW][ROWS][16]
+    __shared__ float tval[ROWS][TILE];
+    __shared__ uint32_t tkey[ROWS][TILE];
+
+    const int g = blockIdx.x % a.tiles, split = blockIdx.x / a.tiles;
+    const SegDev& sg = a.seg[0];
+    int t = g - sg.tile_begin;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    // the expert gather, as dr_gemv_moe's (the rows modes past two rows)
     UnionLds* ul = nullptr;
     if constexpr (MOE == DR_MOE_GATE_UP_ROWS || MOE == DR_MOE_DOWN_ROWS) {
         ul = union_lds<MOE>();
@@ -1121,13 +1231,7 @@ __global__ __launch_bounds__(512) void dr_mfma(const Args a) {
 #pragma unroll
         for (int tt = 0; tt < MT; ++tt) acc[q][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
     auto chunk = [&](const Args& b, const uint8_t* const* cbx, const uint8_t* const* ebx, int k0, int k1) {
-        if (fmt == DR_BFP8) {
-            for (int gg = k0 >> 8; gg < (k1 >> 8); ++gg) mgroup_bfp8<MT, PW>(b, cbx, ebx, gg, lane, acc);
-        } else if (fmt == DR_BFP4) {
-            for (int gg = k0 >> 8; gg < (k1 >> 8); ++gg) mgroup_bfp4<MT, PW>(b, cbx, ebx, gg, lane, acc);
-        } else {
-            for (int b0 = k0 / 32; b0 < k1 / 32; b0 += 4) mgroup_bf16<MT, PW>(b, cbx, b0, lane, acc);
-        }
+        for (int gg = k0 >> 8; gg < (k1 >> 8); ++gg) mgroup_bfp4<MT, PW>(b, cbx, ebx, gg, lane, acc);
     };
     const int ch1 = min((split + 1) * a.cps, a.chunks);
     for (int ch = split * a.cps + wave; ch < ch1; ch += a.waves) {
@@ -1137,7 +1241,7 @@ __global__ __launch_bounds__(512) void dr_mfma(const Args a) {
             int e = MOE == DR_MOE_DOWN ? moe_id(a, 0, s) : (s < ul->count ? (int)ul->list[s] : -1);
             e = __builtin_amdgcn_readfirstlane(e);
             if (e < 0) continue;
-            Args b = a;
+            Args b = a;  // (the chunk's view of x: the unit's block)
             b.x = a.x + (size_t)s * a.ek;
             b.k = a.ek;
             b.k_pad = a.ekp;
@@ -1454,22 +1558,22 @@ void launch_mfma(const Args& a, int grid, hipStream_t st) {
 }
 
 template <int MR, int PW, int MOE>
-void launch_gemv_moe(const Args& a, int grid, hipStream_t st) {
+void launch_gemv_moe(const MoeArgs& a, int grid, hipStream_t st) {
     const dim3 b(64 * a.waves);
     const size_t lds = (size_t)max(a.waves, a.splits) * PW * MR * 16 * sizeof(float);
-    hipLaunchKernelGGL((dr_gemv<MR, PW, DR_BFP4, true, MOE>), dim3(grid), b, lds, st, a);
+    hipLaunchKernelGGL((dr_gemv_moe<MR, PW, MOE>), dim3(grid), b, lds, st, a);
 }
 
 template <int MT, int PW, int MOE>
-void launch_mfma_moe(const Args& a, int grid, hipStream_t st) {
+void launch_mfma_moe(const MoeArgs& a, int grid, hipStream_t st) {
     const dim3 b(64 * a.waves);
     const size_t lds = (size_t)max(a.waves, a.splits) * PW * 16 * MT * 16 * sizeof(float);
-    hipLaunchKernelGGL((dr_mfma<MT, PW, DR_BFP4, true, MOE>), dim3(grid), b, lds, st, a);
+    hipLaunchKernelGGL((dr_mfma_moe<MT, PW, MOE>), dim3(grid), b, lds, st, a);
 }
 
 // one pass of an expert-gathered launch (bfloat4_b): the one-row modes on the GEMV; the rows modes on the GEMV up to
 // two rows, else the MFMA kernel (16 rows a pass for gate/up, 16 or 32 for down)
-hipError_t launch_moe(const Args& a, int mode, int rows, int grid, hipStream_t st) {
+hipError_t launch_moe(const MoeArgs& a, int mode, int rows, int grid, hipStream_t st) {
     switch (mode) {
         case DR_MOE_GATE_UP: launch_gemv_moe<1, 4, DR_MOE_GATE_UP>(a, grid, st); break;
         case DR_MOE_DOWN: launch_gemv_moe<1, 2, DR_MOE_DOWN>(a, grid, st); break;
@@ -1610,7 +1714,7 @@ int prepare(const dr_launch* L, Args& a, int& pw, int& tiles, int& mr) {
     a.ldr = L->ldr;
     a.res_mode = L->residual ? (L->residual_mode == 2 ? 2 : 1) : 0;
     a.act = L->act;
-    if (a.act < DR_ACT_SILU || a.act > DR_ACT_SWIGLU_OAI) return DR_EINVAL;
+    if (a.act < DR_ACT_SILU || a.act > DR_ACT_SWIGLU_OAI) return DR_EINVAL;  // (swiglu_oai: the expert gather only)
     a.nseg = L->nseg;
     pw = L->seg[0].glu ? 4 : 2;
     tiles = 0;
@@ -1683,6 +1787,7 @@ extern "C" {
 int64_t dr_workspace_bytes(const dr_launch* L) {
     Args a{};
     int pw, tiles, mr;
+    if (L != nullptr && L->act == DR_ACT_SWIGLU_OAI) return -1;  // (the dense GLU: silu or gelu_tanh)
     if (prepare(L, a, pw, tiles, mr) != DR_OK) return -1;
     return workspace_bytes(a, pw, mr);
 }
@@ -1690,6 +1795,7 @@ int64_t dr_workspace_bytes(const dr_launch* L) {
 int dr_matmul(const dr_launch* L) {
     Args a{};
     int pw, tiles, mr;
+    if (L != nullptr && L->act == DR_ACT_SWIGLU_OAI) return DR_EINVAL;  // (the dense GLU: silu or gelu_tanh)
     const int st0 = prepare(L, a, pw, tiles, mr);
     if (st0 != DR_OK) return st0;
     const int64_t need = workspace_bytes(a, pw, mr);
@@ -1760,7 +1866,7 @@ namespace {
 
 // the base launch's arguments (prepare), then the gather's: the tiles of the gate/up modes, the gathered K of the
 // down modes, the rows a pass
-int prepare_moe(const dr_launch* L, const dr_moe* M, Args& a, int& pw, int& tiles, int& mr) {
+int prepare_moe(const dr_launch* L, const dr_moe* M, MoeArgs& a, int& pw, int& tiles, int& mr) {
     if (L == nullptr || M == nullptr || M->mode < DR_MOE_GATE_UP || M->mode > DR_MOE_DOWN_ROWS) return DR_EINVAL;
     const int mode = M->mode;
     const bool nmode = mode == DR_MOE_GATE_UP || mode == DR_MOE_GATE_UP_ROWS;
@@ -1827,14 +1933,14 @@ int prepare_moe(const dr_launch* L, const dr_moe* M, Args& a, int& pw, int& tile
 extern "C" {
 
 int64_t dr_moe_workspace_bytes(const dr_launch* L, const dr_moe* M) {
-    Args a{};
+    MoeArgs a{};
     int pw, tiles, mr;
     if (prepare_moe(L, M, a, pw, tiles, mr) != DR_OK) return -1;
     return workspace_bytes(a, pw, mr);
 }
 
 int dr_moe_matmul(const dr_launch* L, const dr_moe* M) {
-    Args a{};
+    MoeArgs a{};
     int pw, tiles, mr;
     const int st0 = prepare_moe(L, M, a, pw, tiles, mr);
     if (st0 != DR_OK) return st0;
@@ -1847,7 +1953,7 @@ int dr_moe_matmul(const dr_launch* L, const dr_moe* M) {
     hipStream_t st = S(L->stream);
     const size_t ysz = a.y_f32 ? 4 : 2;
     for (int r0 = 0; r0 < L->m; r0 += mr) {
-        Args p = a;
+        MoeArgs p = a;
         p.m = L->m - r0 < mr ? L->m - r0 : mr;
         p.x = a.x + (size_t)r0 * a.ldx;
         p.y = reinterpret_cast<uint8_t*>(L->y) + (size_t)r0 * a.ldy * ysz;

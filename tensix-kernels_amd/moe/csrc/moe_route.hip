@@ -5,7 +5,7 @@
 // groups. Then k rounds each take the best untaken key across the wavefront (a butterfly over the lanes' own bests,
 // the lower id first among equal keys). The weights come last, in double, rounded to bf16 once: the softmax over the
 // picked logits, or the picks' sigmoids (over their sum when normalized), times the scale. This replaces
-// moe/kernels/moe_route.cpp's fixed-point arithmetic on one RISC-V core (moe/moe8.py:1145-1257).
+// moe/kernels/moe_route.cpp's fixed-point arithmetic on one RISC-V core (moe/moe8.py:1139-1253).
 
 #include <hip/hip_runtime.h>
 

@@ -48,7 +48,7 @@ DR_BFP4 = 1
 ACTS = {"silu": 0, "gelu_tanh": 1, "swiglu_oai": 2}
 OAI_ALPHA, OAI_LIMIT = 1.702, 7.0
 
-# --- settings (module attributes of the reference, moe8.py:85-111): the Tensix work split; they change nothing here
+# --- settings (module attributes of the reference, moe8.py:73-91): the Tensix work split; they change nothing here
 ROWS_SFPU = True
 GU_CPB = 0
 GU_ROWS_CPB = 0
@@ -66,7 +66,7 @@ PackCacheMismatch = pc.PackCacheMismatch
 
 def sigmoid_table():
     """The reference route kernel's bounds table: sigmoid(i / 16 - 16), i = 0 .. 512, in Q2.30, rounded (reference
-    moe8.py:104-108). The router here computes in double and does not need it; it is kept for code that reads it."""
+    moe8.py:108-114). The router here computes in double and does not need it; it is kept for code that reads it."""
     return [round((1.0 / (1.0 + math.exp(-(i / 16 - 16)))) * (1 << 30)) for i in range(513)]
 
 
@@ -90,7 +90,7 @@ def bfp4_tiles(w, kblock=False):
     (shifted-out bits not sticky), at most 7; zero and denormal inputs give 0 and the sign stays only on a non-zero
     magnitude. 64 exponent bytes (face by face, row by row), then two codes a byte (the first in the low nibble).
     kblock: each tile holds its block transposed, so a face row is 16 consecutive K at one N (reference
-    moe8.py:116-154)."""
+    moe8.py:117-154)."""
     w = np.ascontiguousarray(w.float().numpy() if isinstance(w, torch.Tensor) else w, np.float32)
     k, n = w.shape
     assert k % TILE == 0 and n % TILE == 0, w.shape
@@ -128,7 +128,7 @@ def bfp4_values(tiles, kblock=False):
 
 def gu_groups(it, banks):
     """(G, GW): the reference's gate_up column groups per expert and bank, and their width in tiles (reference
-    moe8.py:207-217). Here a Tensix dest-size rule only: the layout does not depend on it, but gate_up refuses column
+    moe8.py:204-212). Here a Tensix dest-size rule only: the layout does not depend on it, but gate_up refuses column
     groups with one loader as the reference does."""
     ncmax = 2 * -(-it // banks)
     if ncmax <= GW_MAX:
@@ -137,7 +137,7 @@ def gu_groups(it, banks):
 
 
 def _clamp_cpb(device, banks, cores_per_bank):
-    """cores_per_bank capped at the grid's share of a bank (reference moe8.py:511-513)."""
+    """cores_per_bank capped at the grid's share of a bank (reference moe8.py:502-504)."""
     g = dev.as_device(device).compute_with_storage_grid_size()
     return max(1, min(cores_per_bank, (g.x * g.y) // banks))
 
@@ -193,7 +193,7 @@ def _pack_device(d, gate_up, down, gu_bias=None):
 
 
 def _meta(E, H, I, banks, cpb, gate_up, down, gu_bias, kblock):
-    """The pack cache's meta: what the packed arrays depend on (reference moe8.py:361-376)."""
+    """The pack cache's meta: what the packed arrays depend on (reference moe8.py:349-376)."""
     meta = {
         "version": PACK_VERSION,
         "layout": LAYOUT,
@@ -242,7 +242,7 @@ def _check_weights(gate_up, down, gu_bias, kblock):
 def pack_host(gate_up, down, banks, cores_per_bank=3, cache=None, gu_bias=None, rebuild=False, kblock=False):
     """pack()'s arrays on the host: a dict of numpy arrays and numbers that pack_upload puts on a device. The packing
     itself runs on the current GPU. Keys: version, E, H, I, banks, cpb, gu, gu_exps, dn, dn_exps, bias (or absent),
-    gu_bias (bool), kblock (bool). cache, gu_bias, rebuild: as pack()'s (reference moe8.py:435-466)."""
+    gu_bias (bool), kblock (bool). cache, gu_bias, rebuild: as pack()'s (reference moe8.py:435-465)."""
     E, H, I = _check_weights(gate_up, down, gu_bias, kblock)
     meta = _meta(E, H, I, banks, cores_per_bank, gate_up, down, gu_bias, kblock)
     arrays = None
@@ -261,7 +261,7 @@ def pack_host(gate_up, down, banks, cores_per_bank=3, cache=None, gu_bias=None, 
 
 
 def pack_upload(device, host):
-    """pack_host's dict on the device: the dict the ops take (reference moe8.py:469-508)."""
+    """pack_host's dict on the device: the dict the ops take (reference moe8.py:468-499)."""
     assert host["version"] == PACK_VERSION, (host["version"], PACK_VERSION)
     d = dev.as_device(device)
     banks, cpb = host["banks"], host["cpb"]
@@ -310,7 +310,7 @@ def pack(device, gate_up, down, cores_per_bank=3, banks=None, cache=None, gu_bia
     is; rebuild=True packs again and writes over it.
 
     gu_bias: [E, 2I] as [up | gate], added to x U and x G before the activation, held in bf16. kblock (exponents
-    along K) is not supported and raises (reference moe8.py:516-544)."""
+    along K) is not supported and raises (reference moe8.py:507-527)."""
     d = dev.as_device(device)
     banks = banks or dev.dram_banks(d)
     cpb = _clamp_cpb(d, banks, cores_per_bank)
@@ -336,7 +336,7 @@ def pack_cached(device, cache, cores_per_bank=3, banks=None, kblock=False, gu_bi
     version, the banks and cores per bank (clamped to the device as pack() does), kblock, and the bias (gu_bias None:
     the cache has none; True: it has one; a tensor: its fingerprint must equal the cache's). verify: every array's
     sha256 against sums.json (a cache without one is refused unless verify=False). Anything that differs raises
-    PackCacheMismatch and nothing is changed (reference moe8.py:547-624)."""
+    PackCacheMismatch and nothing is changed (reference moe8.py:530-604)."""
     path = Path(cache)
     try:
         meta = json.loads((path / "meta.json").read_text())
@@ -406,7 +406,7 @@ def repack_down(cache, cores_per_bank=2):
 def _glu(g, u, act):
     """The GLU of the pre-activations (float64 tensors): act(g) * u, act silu, gelu_tanh (HF's gelu_pytorch_tanh), or
     the clamped SwiGLU of gpt-oss, where g is capped at 7 and u clamped to +-7 then shifted by 1 (reference
-    moe8.py:629-639)."""
+    moe8.py:607-616)."""
     assert act in ACTS, f"moe8: act {act!r}"
     if act == "swiglu_oai":
         gc = torch.clamp(g, max=OAI_LIMIT)
@@ -418,7 +418,7 @@ def _glu(g, u, act):
 def reference(x, gate_up, down, ids, w, act="silu", gu_bias=None):
     """(y [1, H], h [1, k * I]) in float64 for one row: h's slot s = w_s * GLU(x G_e + b_g, x U_e + b_u) of expert
     e = ids[s], y = sum over the slots of h_s @ D_e. gate_up [E, H, 2I] as [up | gate], down [E, I, H], used as given;
-    gu_bias [E, 2I] as [up | gate], rounded to bf16 as packed (reference moe8.py:642-660)."""
+    gu_bias [E, 2I] as [up | gate], rounded to bf16 as packed (reference moe8.py:619-636)."""
     I = gate_up.shape[-1] // 2
     chosen = [int(e) for e in ids]
     xd = x.reshape(-1).double()
@@ -432,18 +432,18 @@ def reference(x, gate_up, down, ids, w, act="silu", gu_bias=None):
 
 
 def reference_rows(x, gate_up, down, ids, w, act="silu", gu_bias=None):
-    """y [R, H] in float64: row r's reference() with its own ids[r] and w[r] (reference moe8.py:663-669)."""
+    """y [R, H] in float64: row r's reference() with its own ids[r] and w[r] (reference moe8.py:639-644)."""
     rows = [reference(x[r], gate_up, down, ids[r], w[r], act, gu_bias)[0] for r in range(len(ids))]
     return torch.cat(rows, dim=0)
 
 
 def union(ids, E):
-    """The ids' distinct experts below E in increasing order (the kernels' union; reference moe8.py:672-674)."""
+    """The ids' distinct experts below E in increasing order (the kernels' union; reference moe8.py:647-649)."""
     return sorted({int(e) for e in torch.as_tensor(ids).reshape(-1).tolist() if 0 <= int(e) < E})
 
 
 def u_max(P, rows, k):
-    """The most experts the union of rows x k ids can hold: h's width is u_max(...) * I (reference moe8.py:915-917)."""
+    """The most experts the union of rows x k ids can hold: h's width is u_max(...) * I (reference moe8.py:923-925)."""
     return min(P["E"], rows * k)
 
 
@@ -457,7 +457,7 @@ def _loaders(loaders, default):
 
 
 def _gu_cpb(P, cpb, default=0):
-    """gate_up's cores per bank (reference moe8.py:689-698): a work split only; checked as there."""
+    """gate_up's cores per bank (reference moe8.py:693-701): a work split only; checked as there."""
     g = P["device"].compute_with_storage_grid_size()
     most = (g.x * g.y) // P["banks"]
     if not cpb:
@@ -536,7 +536,7 @@ def gate_up(x, P, ids, w, k, *, ids32=False, kw=8, fidelity="hifi2", memory_conf
     ids[s] (a slot whose id is not below E: zeros). x [1, 1, 1, H] bf16; ids [..., k] uint16 (uint32 with ids32) and
     w [..., k] bf16 on the GPU, their first row used. cpb, loaders, kw, fidelity: the reference's work split,
     checked as there and changing nothing; column groups and a bias need loaders=2 as there. act: "silu", "gelu_tanh"
-    or "swiglu_oai" (reference moe8.py:710-815)."""
+    or "swiglu_oai" (reference moe8.py:710-817)."""
     assert act in ACTS, f"moe8: act {act!r}"
     assert 1 <= k <= 16, k
     H, I = P["H"], P["I"]
@@ -552,7 +552,7 @@ def gate_up(x, P, ids, w, k, *, ids32=False, kw=8, fidelity="hifi2", memory_conf
 
 def down(h, P, ids, k, *, ids32=False, kw=8, fidelity="hifi2", memory_config=None, loaders=None):
     """y [1, 1, 1, H] bf16 = h @ the chosen experts' down rows (slot s's I values of h times expert ids[s]'s I rows;
-    a slot whose id is not below E adds nothing). h [1, 1, 1, k * I] bf16 (gate_up's) (reference moe8.py:818-900)."""
+    a slot whose id is not below E adds nothing). h [1, 1, 1, k * I] bf16 (gate_up's) (reference moe8.py:820-910)."""
     assert 1 <= k <= 16, k
     _loaders(loaders, LOADERS)
     H, I = P["H"], P["I"]
@@ -571,7 +571,7 @@ def gate_up_rows(x, P, ids, w, k, rows, *, ids32=False, kw=8, fidelity="hifi2", 
     """h [1, 1, 32, u_max * I] bf16 for x's first `rows` rows: union index q's I columns hold row r's routing weight
     for expert union(ids)[q] times act(x_r G + b_g) * (x_r U + b_u) (0 where row r did not choose it); rows past
     `rows` and columns past the union are 0. ids [1, 1, >= rows, k] uint16 (uint32 with ids32) and w [1, 1, >= rows,
-    k] bf16, their first `rows` rows (reference moe8.py:925-1036)."""
+    k] bf16, their first `rows` rows (reference moe8.py:928-1037)."""
     assert act in ACTS, f"moe8: act {act!r}"
     _rows_args(rows, k)
     _loaders(loaders, ROWS_LOADERS)
@@ -586,7 +586,7 @@ def gate_up_rows(x, P, ids, w, k, rows, *, ids32=False, kw=8, fidelity="hifi2", 
 def down_rows(h, P, ids, k, rows, *, ids32=False, kw=8, fidelity="hifi2", memory_config=None, loaders=None):
     """y [1, 1, 32, H] bf16: row r = the sum over the union of the rows x k ids of h's row r (union index q's I
     columns) times expert union(ids)[q]'s down rows; rows past `rows` are 0. h is gate_up_rows' (the same ids, rows
-    and k) (reference moe8.py:1039-1139)."""
+    and k) (reference moe8.py:1040-1136)."""
     _rows_args(rows, k)
     _loaders(loaders, ROWS_LOADERS)
     H, I = P["H"], P["I"]
@@ -612,7 +612,7 @@ def route(logits, ids, w, k, *, kind="softmax", bias=None, ids32=False, experts=
     shared: [1, 1, R, 1] bf16 that gets sigmoid(logits[:, E]). scale: every weight times it (0 < scale < 4). groups=
     (n_group, topk_group) (sigmoid with a bias): a group's score the sum of its two largest keys, the topk_group best
     groups kept (the lower group first among equal scores). slot: an id written as slot k of every row at weight 1.0.
-    Keys and weights in double, rounded to bf16 at the end. Returns w (reference moe8.py:1145-1257)."""
+    Keys and weights in double, rounded to bf16 at the end. Returns w (reference moe8.py:1139-1253)."""
     assert kind in ("softmax", "sigmoid"), f"moe8.route: kind {kind!r}"
     R, W = logits.shape[-2], logits.shape[-1]
     E = experts or W
@@ -655,7 +655,7 @@ def route_reference(logits, k, kind="softmax", bias=None, scale=1.0, norm=True, 
     lower id first among equal keys (a stable sort). Keys: the logits (softmax, or sigmoid without a bias), else
     sigmoid + bias; groups: a group's score the sum of its two largest keys, the topk_group best groups (the lower
     first among equal scores) keeping their keys, the rest -inf. slot: one more column of that id at weight 1.0
-    (reference moe8.py:1260-1286)."""
+    (reference moe8.py:1256-1286)."""
     lg = logits.double()
     R, E = lg.shape
     sg = torch.sigmoid(lg)

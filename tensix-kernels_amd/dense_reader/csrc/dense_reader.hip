@@ -166,6 +166,18 @@ __device__ __forceinline__ uint32_t x_bits(const Args& a, int m, int k) {
     return v & opaque((m < a.m && k < a.k) ? 0xFFFFFFFFu : 0u);
 }
 
+// Weight codes, exponents and group scales are read once a launch: non-temporal loads (the nt bit) stream them past
+// the caches that x and the partial sums reuse. Measured on MI355X against plain loads: the north-star shape 13.3 ->
+// 12.3 us, the bfloat4_b GLU pair 16.7 -> 15.1 us, the MFMA kernel 5 % and the LM head 4 % faster.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_stream16(const uint8_t* p) {
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t ld_stream4(const uint8_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+}
+
 template <int PW>
 struct Codes {
     uint4 c[PW];
@@ -206,12 +218,12 @@ __device__ __forceinline__ void chunk_bfp8(const Args& a, const uint8_t* const* 
     for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int q = 0; q < PW; ++q)
-            e[h][q] = *reinterpret_cast<const uint32_t*>(eb[q] + (uint32_t)((h ? g1 : g0) * 256 + 4 * lane));
+            e[h][q] = ld_stream4(eb[q] + (uint32_t)((h ? g1 : g0) * 256 + 4 * lane));
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
         const int b = 4 * (u < 4 ? g0 : g1) + (u & 3);
 #pragma unroll
-        for (int q = 0; q < PW; ++q) c[u].c[q] = *reinterpret_cast<const uint4*>(cb[q] + (uint32_t)(b * 1024 + lane * 16));
+        for (int q = 0; q < PW; ++q) c[u].c[q] = ld_stream16(cb[q] + (uint32_t)(b * 1024 + lane * 16));
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
@@ -283,12 +295,12 @@ __device__ __forceinline__ void chunk_bfp4(const Args& a, const uint8_t* const* 
     for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int q = 0; q < PW; ++q)
-            e[h][q] = *reinterpret_cast<const uint32_t*>(eb[q] + (uint32_t)((h ? g1 : g0) * 256 + 4 * lane));
+            e[h][q] = ld_stream4(eb[q] + (uint32_t)((h ? g1 : g0) * 256 + 4 * lane));
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
         const int b = 2 * (u < 2 ? g0 : g1) + (u & 1);
 #pragma unroll
-        for (int q = 0; q < PW; ++q) c[u].c[q] = *reinterpret_cast<const uint4*>(cb[q] + (uint32_t)(b * 1024 + lane * 16));
+        for (int q = 0; q < PW; ++q) c[u].c[q] = ld_stream16(cb[q] + (uint32_t)(b * 1024 + lane * 16));
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -342,13 +354,13 @@ __device__ __forceinline__ void chunk_int4(const Args& a, const uint8_t* const* 
     for (int u = 0; u < 4; ++u) {
         const int b = 2 * (u < 2 ? g0 : g1) + (u & 1);
 #pragma unroll
-        for (int q = 0; q < PW; ++q) sc[u][q] = gs[q][(size_t)b * 64 + lane];
+        for (int q = 0; q < PW; ++q) sc[u][q] = __builtin_nontemporal_load(gs[q] + (size_t)b * 64 + lane);
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
         const int b = 2 * (u < 2 ? g0 : g1) + (u & 1);
 #pragma unroll
-        for (int q = 0; q < PW; ++q) c[u].c[q] = *reinterpret_cast<const uint4*>(cb[q] + (uint32_t)(b * 1024 + lane * 16));
+        for (int q = 0; q < PW; ++q) c[u].c[q] = ld_stream16(cb[q] + (uint32_t)(b * 1024 + lane * 16));
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -405,7 +417,7 @@ __device__ __forceinline__ void chunk_bf16(const Args& a, const uint8_t* const* 
         for (int u = 0; u < G; ++u)
 #pragma unroll
             for (int q = 0; q < PW; ++q)
-                c[u][q] = *reinterpret_cast<const uint4*>(cb[q] + (uint32_t)((gb + u) * 1024 + lane * 16));
+                c[u][q] = ld_stream16(cb[q] + (uint32_t)((gb + u) * 1024 + lane * 16));
 #pragma unroll
         for (int u = 0; u < G; ++u)
 #pragma unroll
@@ -1008,12 +1020,12 @@ __device__ __forceinline__ void mgroup_bfp8(const Args& a, const uint8_t* const*
 #pragma unroll
             for (int tt = 0; tt < MT; ++tt) A[b][h][tt] = x_row8(a, 16 * tt + r, (4 * g + b) * 64 + 16 * kq + 8 * h);
 #pragma unroll
-    for (int q = 0; q < PW; ++q) e[q] = *reinterpret_cast<const uint32_t*>(eb[q] + (uint32_t)(g * 256 + 4 * lane));
+    for (int q = 0; q < PW; ++q) e[q] = ld_stream4(eb[q] + (uint32_t)(g * 256 + 4 * lane));
 #pragma unroll
     for (int b = 0; b < 4; ++b)
 #pragma unroll
         for (int q = 0; q < PW; ++q)
-            c[b][q] = *reinterpret_cast<const uint4*>(cb[q] + (uint32_t)((4 * g + b) * 1024 + lane * 16));
+            c[b][q] = ld_stream16(cb[q] + (uint32_t)((4 * g + b) * 1024 + lane * 16));
     if (a.k != a.k_pad && (g + 1) * 256 > a.k) {  // (a ragged K's last group only)
 #pragma unroll
         for (int b = 0; b < 4; ++b)
@@ -1077,12 +1089,12 @@ __device__ __forceinline__ void mgroup_bfp4(const Args& a, const uint8_t* const*
 #pragma unroll
             for (int tt = 0; tt < MT; ++tt) A[b][d][tt] = x_row8(a, 16 * tt + r, (2 * g + b) * 128 + 32 * kq + 8 * d);
 #pragma unroll
-    for (int q = 0; q < PW; ++q) e[q] = *reinterpret_cast<const uint32_t*>(eb[q] + (uint32_t)(g * 256 + 4 * lane));
+    for (int q = 0; q < PW; ++q) e[q] = ld_stream4(eb[q] + (uint32_t)(g * 256 + 4 * lane));
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
         for (int q = 0; q < PW; ++q)
-            c[b][q] = *reinterpret_cast<const uint4*>(cb[q] + (uint32_t)((2 * g + b) * 1024 + lane * 16));
+            c[b][q] = ld_stream16(cb[q] + (uint32_t)((2 * g + b) * 1024 + lane * 16));
     if (a.k != a.k_pad && (g + 1) * 256 > a.k) {  // (a ragged K's last group only)
 #pragma unroll
         for (int b = 0; b < 2; ++b)
@@ -1127,7 +1139,7 @@ __device__ __forceinline__ void mgroup_bf16(const Args& a, const uint8_t* const*
 #pragma unroll
     for (int u = 0; u < 4; ++u)
 #pragma unroll
-        for (int q = 0; q < PW; ++q) c[u][q] = *reinterpret_cast<const uint4*>(cb[q] + (uint32_t)((b0 + u) * 1024 + lane * 16));
+        for (int q = 0; q < PW; ++q) c[u][q] = ld_stream16(cb[q] + (uint32_t)((b0 + u) * 1024 + lane * 16));
     if (a.k != a.k_pad && (b0 + 4) * 32 > a.k) {  // (a ragged K's last blocks only)
 #pragma unroll
         for (int u = 0; u < 4; ++u)

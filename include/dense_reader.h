@@ -139,7 +139,8 @@ int64_t dr_workspace_bytes(const dr_launch* launch);
 int dr_matmul(const dr_launch* launch);
 
 /* The best k_out of records [n_records][2 * rows * k] (as dr_topk writes them) per row: vals [rows][k_out] fp32
- * (-inf empty), ids [rows][k_out] int32 (-1 empty), highest first, ties to the lower id. k_out <= 64. Many records
+ * (-inf empty), ids [rows][k_out] int32 (-1 empty), highest first, ties to the lower id. rows <= 32 (a record's, as
+ * dr_topk's), k_out <= 64. Many records
  * are merged by several workgroups a row that meet in the workspace (dr_topk_merge_workspace_bytes; zeroed once by
  * the caller, left with its counters at zero; merges sharing one must not overlap in time). */
 int64_t dr_topk_merge_workspace_bytes(int n_records, int rows, int k);

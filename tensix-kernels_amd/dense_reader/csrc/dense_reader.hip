@@ -1466,6 +1466,7 @@ constexpr int MERGE_MAXK = 64;  // k_out at most: one list is one value a lane
 
 using namespace wsel;
 
+template <bool NARROW>  // k_out <= 32
 __global__ __launch_bounds__(SEL_T) void dr_merge_k(SelArgs A, int fp32, float* __restrict__ vals,
                                                     int32_t* __restrict__ ids) {
     __shared__ SelShared sh;
@@ -1473,7 +1474,7 @@ __global__ __launch_bounds__(SEL_T) void dr_merge_k(SelArgs A, int fp32, float* 
     const int lane = threadIdx.x & 63;
     unsigned long long list;
     int count;
-    const bool mine = select_row(
+    const bool mine = select_row<NARROW>(
         A, r, sl,
         [fp32](uint32_t key, uint32_t id, uint32_t) -> unsigned long long {
             if (id == 0xFFFFFFFFu || (!fp32 && key == 0u)) return 0ull;
@@ -1835,26 +1836,23 @@ int dr_matmul(const dr_launch* L) {
 }
 
 int64_t dr_topk_merge_workspace_bytes(int n_records, int rows, int k) {
-    if (n_records < 1 || rows < 1 || k < 1) return -1;
+    if (n_records < 1 || rows < 1 || rows > SEL_MAXROWS || k < 1) return -1;
     return select_workspace_bytes(n_records, rows, k);
 }
 
 int dr_topk_merge(const void* records, int n_records, int rows, int k, int fp32, int k_out, float* vals,
                   int32_t* ids, void* workspace, int64_t workspace_bytes, void* stream) {
-    if (records == nullptr || vals == nullptr || ids == nullptr || n_records < 1 || rows < 1 || k < 1 || k_out < 1 ||
-        k_out > MERGE_MAXK)
+    if (records == nullptr || vals == nullptr || ids == nullptr || n_records < 1 || rows < 1 || rows > SEL_MAXROWS ||
+        k < 1 || k_out < 1 || k_out > MERGE_MAXK)
         return DR_EINVAL;
     if ((int64_t)n_records * k > ((int64_t)1 << 40)) return DR_ERANGE;
-    SelArgs A{reinterpret_cast<const uint32_t*>(records), n_records, rows, k, k_out, 1, 0, nullptr, nullptr};
+    SelArgs A{reinterpret_cast<const uint32_t*>(records), n_records, rows, k, k_out, 1, 0, nullptr, nullptr, nullptr};
     select_plan(n_records, k, &A.slices, &A.cs);
-    const int64_t need = select_workspace_bytes(n_records, rows, k);
-    if (need > 0) {
-        if (workspace == nullptr || workspace_bytes < need) return DR_EINVAL;
-        A.counters = reinterpret_cast<uint32_t*>(workspace);
-        A.wlist = reinterpret_cast<unsigned long long*>(reinterpret_cast<uint8_t*>(workspace) +
-                                                        select_counter_bytes(rows));
-    }
-    hipLaunchKernelGGL(dr_merge_k, dim3(rows * A.slices), dim3(SEL_T), 0, S(stream), A, fp32, vals, ids);
+    if (!select_bind(A, workspace, workspace_bytes)) return DR_EINVAL;
+    if (k_out <= 32)
+        hipLaunchKernelGGL(dr_merge_k<true>, dim3(rows * A.slices), dim3(SEL_T), 0, S(stream), A, fp32, vals, ids);
+    else
+        hipLaunchKernelGGL(dr_merge_k<false>, dim3(rows * A.slices), dim3(SEL_T), 0, S(stream), A, fp32, vals, ids);
     return hip_status(hipGetLastError());
 }
 

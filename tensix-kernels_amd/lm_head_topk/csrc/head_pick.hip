@@ -58,6 +58,9 @@ __device__ __forceinline__ uint32_t slot_id(const SelArgs& A, int r, uint32_t c)
     return A.rec[(size_t)p * 2 * A.rows * A.k + (size_t)A.rows * A.k + (size_t)r * A.k + s];
 }
 
+// PACK (slots and vocab below 2^24): a key carries its slot's id in its low 24 bits (the 16-bit key, then the slot's
+// index complemented in 24 bits, then the id), so the candidates' ids need no second read of the records
+template <bool PACK>
 __global__ __launch_bounds__(SEL_T) void dr_pick_k(SelArgs A, uint32_t vocab, int round_bf16,
                                                    const uint16_t* __restrict__ x, int ldx, int dim,
                                                    const uint16_t* __restrict__ head, long long ld_head,
@@ -72,78 +75,97 @@ __global__ __launch_bounds__(SEL_T) void dr_pick_k(SelArgs A, uint32_t vocab, in
     // 1. the best `top` valid slots by key, the earlier slot first among equals
     unsigned long long list;
     int count;
-    const bool mine = select_row(
+    const bool mine = select_row<true>(
         A, r, sl,
         [vocab](uint32_t key, uint32_t id, uint32_t c) -> unsigned long long {
             key &= 0xFFFFu;
             if (key == 0u || id >= vocab) return 0ull;
-            return ((unsigned long long)key << 32) | (unsigned long long)(0xFFFFFFFFu - c);
+            if constexpr (PACK)
+                return ((unsigned long long)key << 48) | ((unsigned long long)(0xFFFFFFu - c) << 24) | id;
+            else
+                return ((unsigned long long)key << 32) | (unsigned long long)(0xFFFFFFFFu - c);
         },
         sh, list, count);
     if (!mine) return;
     if (wave == 0) {
         const bool have = lane < A.keep && list != 0ull;
         const int n = __popcll(__ballot(have));
-        if (lane < MAXTOP) cid[lane] = have ? slot_id(A, r, 0xFFFFFFFFu - (uint32_t)(list & 0xFFFFFFFFu)) : 0xFFFFFFFFu;
+        uint32_t id = 0xFFFFFFFFu;
+        if (have) id = PACK ? (uint32_t)(list & 0xFFFFFFu) : slot_id(A, r, 0xFFFFFFFFu - (uint32_t)(list & 0xFFFFFFFFu));
+        if (lane < MAXTOP) cid[lane] = id;
         if (lane == 0) s_n = n;
     }
     __syncthreads();
     const int n = s_n;
 
     // 2. the candidates' logits: x[r] . head[id], one wavefront a candidate, float32 in a fixed order (lane l sums
-    // d = 8 l + 512 i + j, i then j ascending; then the lanes, a butterfly). Every load of a span of DSPAN values is
-    // issued before the first is used.
-    constexpr int DSPAN = 8 * 512;
+    // d = 8 l + 512 i + j, i then j ascending; then the lanes, a butterfly). A wavefront takes RG candidates at once
+    // (j, j + SEL_W, ...) and issues every load of a span of DSPAN values for all of them before the first is used.
+    constexpr int DSPAN = 8 * 512, RG = 4;
     const uint16_t* xr = x + (size_t)r * ldx;
-    for (int j = wave; j < n; j += SEL_W) {
-        const uint16_t* hr = head + (size_t)cid[j] * (size_t)ld_head;
-        float acc = 0.f;
+    for (int j0 = wave; j0 < n; j0 += RG * SEL_W) {
+        const uint16_t* hr[RG];
+#pragma unroll
+        for (int t = 0; t < RG; ++t)  // (past n: candidate n - 1 again, its sum not kept)
+            hr[t] = head + (size_t)cid[min(j0 + t * SEL_W, n - 1)] * (size_t)ld_head;
+        float acc[RG];
+#pragma unroll
+        for (int t = 0; t < RG; ++t) acc[t] = 0.f;
         for (int s0 = 0; s0 < dim; s0 += DSPAN) {
-            uint4 xv[8], hv[8];
+            uint4 xv[8], hv[RG][8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const int d0 = min(s0 + i * 512 + lane * 8, dim - 8);  // (in bounds; past dim masked below)
                 xv[i] = *reinterpret_cast<const uint4*>(xr + d0);
-                hv[i] = *reinterpret_cast<const uint4*>(hr + d0);
+#pragma unroll
+                for (int t = 0; t < RG; ++t) hv[t][i] = *reinterpret_cast<const uint4*>(hr[t] + d0);
             }
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                if (s0 + i * 512 + lane * 8 >= dim) xv[i] = hv[i] = make_uint4(0u, 0u, 0u, 0u);
-                acc = __builtin_fmaf(bf16_lo(xv[i].x), bf16_lo(hv[i].x), acc);
-                acc = __builtin_fmaf(bf16_hi(xv[i].x), bf16_hi(hv[i].x), acc);
-                acc = __builtin_fmaf(bf16_lo(xv[i].y), bf16_lo(hv[i].y), acc);
-                acc = __builtin_fmaf(bf16_hi(xv[i].y), bf16_hi(hv[i].y), acc);
-                acc = __builtin_fmaf(bf16_lo(xv[i].z), bf16_lo(hv[i].z), acc);
-                acc = __builtin_fmaf(bf16_hi(xv[i].z), bf16_hi(hv[i].z), acc);
-                acc = __builtin_fmaf(bf16_lo(xv[i].w), bf16_lo(hv[i].w), acc);
-                acc = __builtin_fmaf(bf16_hi(xv[i].w), bf16_hi(hv[i].w), acc);
+                const bool past = s0 + i * 512 + lane * 8 >= dim;
+                if (past) xv[i] = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+                for (int t = 0; t < RG; ++t) {
+                    const uint4 h = past ? make_uint4(0u, 0u, 0u, 0u) : hv[t][i];
+                    float a = acc[t];
+                    a = __builtin_fmaf(bf16_lo(xv[i].x), bf16_lo(h.x), a);
+                    a = __builtin_fmaf(bf16_hi(xv[i].x), bf16_hi(h.x), a);
+                    a = __builtin_fmaf(bf16_lo(xv[i].y), bf16_lo(h.y), a);
+                    a = __builtin_fmaf(bf16_hi(xv[i].y), bf16_hi(h.y), a);
+                    a = __builtin_fmaf(bf16_lo(xv[i].z), bf16_lo(h.z), a);
+                    a = __builtin_fmaf(bf16_hi(xv[i].z), bf16_hi(h.z), a);
+                    a = __builtin_fmaf(bf16_lo(xv[i].w), bf16_lo(h.w), a);
+                    a = __builtin_fmaf(bf16_hi(xv[i].w), bf16_hi(h.w), a);
+                    acc[t] = a;
+                }
             }
         }
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
-        if (lane == 0) logit[j] = round_bf16 ? __uint_as_float(bf16_bits(acc) << 16) : acc;
+        for (int t = 0; t < RG; ++t) {
+            const float sum = wave_sum_xor(acc[t]);
+            const int j = j0 + t * SEL_W;
+            if (lane == 0 && j < n) logit[j] = round_bf16 ? __uint_as_float(bf16_bits(sum) << 16) : sum;
+        }
     }
     __syncthreads();
 
-    // 3. the pick: the lowest id among the largest logits (lm_head_topk/lmhead.py:40-46)
-    if (threadIdx.x == 0) {
-        uint32_t tok = 0, best_key = 0;
-        bool any = false;
-        for (int j = 0; j < n; ++j) {
-            const uint32_t kk = order32(__float_as_uint(logit[j]));
-            const uint32_t id = cid[j];
-            if (!any || kk > best_key || (kk == best_key && id < tok)) {
-                best_key = kk;
-                tok = id;
-                any = true;
-            }
-        }
+    // 3. the pick: the lowest id among the largest logits (lm_head_topk/lmhead.py:40-46), by a wavefront maximum of
+    // the candidates' (logit rank, id complemented)
+    if (wave == 0) {
+        unsigned long long cand = 0ull;  // (every candidate's is above 0: its rank is)
+        if (lane < n)
+            cand = ((unsigned long long)order32(__float_as_uint(logit[lane])) << 32) | (0xFFFFFFFFu - cid[lane]);
+        const unsigned long long best = wave_max(cand);
         uint32_t* o = out + (size_t)r * 32;
-        o[0] = any ? tok : 0u;
-        o[1] = n > 0 ? cid[0] : 0xFFFFFFFFu;
-        o[2] = (uint32_t)n;
-        for (int w = 3; w < 32; ++w) o[w] = 0u;
-        if (ids_out != nullptr && r == 0) ids_out[0] = o[0];
+        if (lane == 0) {
+            const uint32_t tok = best != 0ull ? 0xFFFFFFFFu - (uint32_t)best : 0u;
+            o[0] = tok;
+            o[1] = n > 0 ? cid[0] : 0xFFFFFFFFu;
+            o[2] = (uint32_t)n;
+            if (ids_out != nullptr && r == 0) ids_out[0] = tok;
+        } else if (lane >= 3 && lane < 32) {
+            o[lane] = 0u;
+        }
     }
 }
 
@@ -154,7 +176,7 @@ __global__ __launch_bounds__(SEL_T) void dr_pick_records_k(SelArgs A, uint32_t v
     const int r = blockIdx.x % A.rows, sl = blockIdx.x / A.rows;
     unsigned long long list;
     int count;
-    const bool mine = select_row(
+    const bool mine = select_row<true>(
         A, r, sl,
         [vocab](uint32_t key, uint32_t id, uint32_t c) -> unsigned long long {
             key &= 0xFFFFu;
@@ -188,16 +210,9 @@ namespace {
 
 int plan_select(SelArgs& A, const void* records, int n_records, int rows, int k, int keep, void* workspace,
                 int64_t workspace_bytes) {
-    A = SelArgs{reinterpret_cast<const uint32_t*>(records), n_records, rows, k, keep, 1, 0, nullptr, nullptr};
+    A = SelArgs{reinterpret_cast<const uint32_t*>(records), n_records, rows, k, keep, 1, 0, nullptr, nullptr, nullptr};
     select_plan(n_records, k, &A.slices, &A.cs);
-    const int64_t need = select_workspace_bytes(n_records, rows, k);
-    if (need > 0) {
-        if (workspace == nullptr || workspace_bytes < need) return DR_EINVAL;
-        A.counters = reinterpret_cast<uint32_t*>(workspace);
-        A.wlist = reinterpret_cast<unsigned long long*>(reinterpret_cast<uint8_t*>(workspace) +
-                                                        select_counter_bytes(rows));
-    }
-    return DR_OK;
+    return select_bind(A, workspace, workspace_bytes) ? DR_OK : DR_EINVAL;
 }
 
 }  // namespace
@@ -214,9 +229,11 @@ int dr_head_pick(const void* records, int n_records, int rows, int k, int top, i
     SelArgs A;
     const int st = plan_select(A, records, n_records, rows, k, top, workspace, workspace_bytes);
     if (st != DR_OK) return st;
-    hipLaunchKernelGGL(dr_pick_k, dim3(rows * A.slices), dim3(SEL_T), 0, S(stream), A, (uint32_t)vocab, round_bf16,
-                       reinterpret_cast<const uint16_t*>(x), ldx, dim, reinterpret_cast<const uint16_t*>(head),
-                       (long long)ld_head, reinterpret_cast<uint32_t*>(out), reinterpret_cast<uint32_t*>(ids_out));
+    const bool pack = (int64_t)n_records * k <= ((int64_t)1 << 24) && vocab <= ((int64_t)1 << 24);
+    hipLaunchKernelGGL(pack ? dr_pick_k<true> : dr_pick_k<false>, dim3(rows * A.slices), dim3(SEL_T), 0, S(stream), A,
+                       (uint32_t)vocab, round_bf16, reinterpret_cast<const uint16_t*>(x), ldx, dim,
+                       reinterpret_cast<const uint16_t*>(head), (long long)ld_head, reinterpret_cast<uint32_t*>(out),
+                       reinterpret_cast<uint32_t*>(ids_out));
     return hipGetLastError() == hipSuccess ? DR_OK : DR_EHIP;
 }
 

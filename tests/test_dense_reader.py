@@ -307,6 +307,10 @@ def test_topk_merge_synthetic(device, fp32):
         (700, 2, 16, 64, np.random.default_rng(7).standard_normal(3000).astype(np.float32)),
         (1, 1, 32, 64, ties),
         (16384, 1, 4, 64, np.random.default_rng(6).standard_normal(9000).astype(np.float32)),  # the most records
+        (4100, 1, 5, 32, ties),  # 21 slices (an odd count: a pair register half empty)
+        (2600, 2, 8, 33, np.random.default_rng(8).standard_normal(5000).astype(np.float32)),  # 33: the 64-wide lists
+        (5000, 1, 9, 1, ties),  # 44 slices, the single best
+        (1200, 3, 7, 31, ties),  # 9 slices
     ):
         t = _records(nrec, rows, k, fp32, nrec + rows, values)
         hv, hi = linear.records_host(t, rows, k, fp32=fp32)

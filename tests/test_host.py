@@ -93,6 +93,10 @@ def test_invalid_arguments_refused_on_the_host():
     assert need >= 4 * 64 * 8 * 2
     assert lib.dr_topk_merge(8, 4008, 4, 8, 0, 32, 8, 8, None, 0, None) == _lib.DR_EINVAL  # workspace missing
     assert lib.dr_topk_merge(8, 4008, 4, 8, 0, 32, 8, 8, 8, need - 1, None) == _lib.DR_EINVAL  # too small
+    # more rows than a record holds (32): refused, so the rows' counters keep their places in a shared workspace
+    assert lib.dr_topk_merge_workspace_bytes(4008, 33, 8) == -1
+    assert lib.dr_topk_merge(8, 4008, 33, 8, 0, 32, 8, 8, 8, 1 << 30, None) == _lib.DR_EINVAL
+    assert lib.dr_topk_merge_workspace_bytes(4008, 32, 8) > lib.dr_topk_merge_workspace_bytes(4008, 1, 8) > 0
     with pytest.raises(ValueError):
         _lib.check(_lib.DR_EINVAL, "x")
     with pytest.raises(RuntimeError):

@@ -20,7 +20,7 @@ import pytest
 import torch
 
 from common.testing import same
-from dense_reader import linear
+from dense_reader import _lib, linear
 from lm_head_topk import head_pick, lmhead
 from oracle import dense_oracle as O
 
@@ -151,6 +151,35 @@ def test_padded_head(device):
     dv = lmhead.DeviceHead(device, w, fmt="bfp4", chunks=CHUNKS, k=k, device_pick=True, valid=valid, rows=short)
     same_tokens(f"padded head (valid {valid}), a table of the valid rows only", dv(tx, rows).numpy(), want, z)
     dv.deallocate()
+    dh.deallocate()
+
+
+def test_pick_ids_from_records(device):
+    """Where the slots or the vocabulary pass 2**24, dr_head_pick reads each candidate's id from the records instead of
+    carrying it in the candidate's key: the same records with a validity bound past 2**24 (every id in them is still
+    below the table's rows, so the same rows are read) must give the same page, word for word, and the oracle's
+    tokens."""
+    w = head(17)
+    rows, k, top = 3, 8, 16
+    x, tx = x_rows(device, rows, 18)
+    dh = lmhead.DeviceHead(device, w, fmt="bfp4", chunks=CHUNKS, k=k, rescore=False)
+    r = dh.logits_topk(tx, rows)
+    rows_t = head_pick.head_rows(device, w)
+    packed = head_pick.pick(r, tx, rows_t, rows, k, top=top).clone()
+    words = head_pick._words(r, rows, k)
+    out = torch.zeros_like(packed)
+    stream = torch.cuda.current_stream(tx.device)
+    wp, wn = head_pick._select_workspace(tx.device, stream, words.shape[0], rows, k)
+    x2 = tx.reshape(-1, DIM)
+    st = _lib.lib().dr_head_pick(words.data_ptr(), words.shape[0], rows, k, top, 1, x2.data_ptr(), DIM, DIM,
+                                 rows_t.data_ptr(), DIM, (1 << 24) + 1, out.data_ptr(), None, wp, wn,
+                                 stream.cuda_stream)
+    _lib.check(st, "dr_head_pick")
+    assert torch.equal(out.cpu(), packed.cpu()), (out.reshape(32, 32)[:rows, :3], packed.reshape(32, 32)[:rows, :3])
+    tok, _, _ = head_pick.tokens(out, rows)
+    want, _, _ = O.pick_from_records(words.cpu().numpy(), rows, k, top, x, w, "bf16", VOCAB)
+    same_tokens("ids read from the records: tokens against the oracle's pick", tok.numpy(), want,
+                O.head_logits(x, w).numpy())
     dh.deallocate()
 
 

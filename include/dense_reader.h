@@ -130,8 +130,10 @@ typedef struct dr_launch {
 } dr_launch;
 
 /* Bytes of workspace the launch needs (0: none; a K long enough to split over several workgroups a tile needs some;
- * -1: the launch is invalid). The workspace is zeroed once when allocated; every launch leaves its counters at zero.
- * Launches that share one workspace must not overlap in time (one stream). */
+ * -1: the launch is invalid). The workspace is zeroed once when allocated; every launch leaves its counters at zero,
+ * and they lie at the same place whatever the launch's shape, so launches of any shape (dr_matmul's and
+ * dr_moe_matmul's) can share one, but not with the top-k merge or the head pick. Launches that share one workspace
+ * must not overlap in time (one stream). */
 int64_t dr_workspace_bytes(const dr_launch* launch);
 
 /* y = the launch's fused matmul. Allocates nothing. A DR_INT4 weight goes alone (one segment, no GLU, residual or
@@ -142,7 +144,8 @@ int dr_matmul(const dr_launch* launch);
  * (-inf empty), ids [rows][k_out] int32 (-1 empty), highest first, ties to the lower id. rows <= 32 (a record's, as
  * dr_topk's), k_out <= 64. Many records
  * are merged by several workgroups a row that meet in the workspace (dr_topk_merge_workspace_bytes; zeroed once by
- * the caller, left with its counters at zero; merges sharing one must not overlap in time). */
+ * the caller; every merge leaves its counters at zero, at the same place whatever its shape, so merges and head picks
+ * of any shape can share one, not overlapping in time). */
 int64_t dr_topk_merge_workspace_bytes(int n_records, int rows, int k);
 int dr_topk_merge(const void* records, int n_records, int rows, int k, int fp32, int k_out, float* vals,
                   int32_t* ids, void* workspace, int64_t workspace_bytes, void* stream);

@@ -14,8 +14,8 @@
  *
  * Both take plain device pointers and a hipStream_t (as void*), allocate nothing, and return DR_OK or a DR_E* status
  * of dense_reader.h. Many records are selected by several workgroups a row that meet in a workspace of
- * dr_topk_merge_workspace_bytes(n_records, rows, k) bytes (dense_reader.h; zeroed once by the caller, left with its
- * counters at zero; launches sharing one must not overlap in time).
+ * dr_topk_merge_workspace_bytes(n_records, rows, k) bytes (dense_reader.h; zeroed once by the caller, its counters
+ * left at zero by every launch; launches sharing one must not overlap in time).
  */
 #ifndef LM_HEAD_H
 #define LM_HEAD_H

@@ -705,7 +705,14 @@ __device__ __forceinline__ void moe_zero(const MoeArgs& a, int t, int unit) {
 // invalidates a whole L2 (it cost 6x the matmul itself). Instead every workspace access is a device-scope atomic
 // (relaxed): such loads and stores go to the device's point of coherence on their own. A workgroup's sums are complete
 // there before it counts itself (each thread waits for its stores, then the barrier), and the last workgroup reads
-// them only after its count has come back.
+// them only after its count has come back. The counters lie at the workspace's start, SPLIT_MAXTILES of them whatever
+// the launch's shape, and the sums after them: a workspace shared by launches of any shape never finds an earlier
+// launch's sums where a counter should be zero (a launch of more tiles runs unsplit).
+#ifndef DR_SPLIT_MAXTILES
+#define DR_SPLIT_MAXTILES 16384
+#endif
+constexpr int SPLIT_MAXTILES = DR_SPLIT_MAXTILES;  // counters in the workspace: tiles of a split launch at most
+
 __device__ __forceinline__ void st_dev(float* p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -1527,6 +1534,15 @@ void plan(int k, int* chunks, int* kch, int* waves, int* splits, int* cps) {
     plan_chunks(k_pad, DR_CHUNK_K ? DR_CHUNK_K : (k_pad >= 4096 ? 512 : 256), chunks, kch, waves, splits, cps);
 }
 
+// a launch of more tiles than the workspace has counters for runs unsplit
+void limit_splits(Args& a) {
+    if (a.splits > 1 && a.tiles > SPLIT_MAXTILES) {
+        a.splits = 1;
+        a.cps = a.chunks;
+        a.waves = a.cps < MAXW ? a.cps : MAXW;
+    }
+}
+
 // the MFMA kernel from this many rows on; below it the GEMV kernel's rows a pass
 #ifndef DR_MFMA_MIN_M
 #define DR_MFMA_MIN_M 3
@@ -1780,6 +1796,7 @@ int prepare(const dr_launch* L, Args& a, int& pw, int& tiles, int& mr) {
     }
     plan(L->k, &a.chunks, &a.kch, &a.waves, &a.splits, &a.cps);
     a.tiles = tiles;
+    limit_splits(a);
     mr = rows_per_pass(L->m);
     if (pw == 4 && mr == 8) mr = 4;    // (GLU: at most 4 GEMV rows or 16 MFMA rows a pass, for the registers
     if (pw == 4 && mr == 32) mr = 16;  // and the LDS)
@@ -1787,11 +1804,17 @@ int prepare(const dr_launch* L, Args& a, int& pw, int& tiles, int& mr) {
     return DR_OK;
 }
 
+// split K's workspace: SPLIT_MAXTILES counters, then every workgroup's column sums
 int64_t workspace_bytes(const Args& a, int pw, int mr) {
     if (a.splits == 1) return 0;
-    const int64_t counters = ((int64_t)a.tiles * 4 + 255) / 256 * 256;
-    return counters + (int64_t)a.tiles * a.splits * pw * mr * 16 * 4;
+    return (int64_t)SPLIT_MAXTILES * 4 + (int64_t)a.tiles * a.splits * pw * mr * 16 * 4;
 }
+
+void bind_split(Args& a, void* workspace) {
+    a.counters = reinterpret_cast<uint32_t*>(workspace);
+    a.wpart = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + (int64_t)SPLIT_MAXTILES * 4);
+}
+
 
 }  // namespace
 
@@ -1816,8 +1839,7 @@ int dr_matmul(const dr_launch* L) {
         // split K needs the workspace: its counters start at zero (the caller zeroes it once; each launch leaves
         // them at zero)
         if (L->workspace == nullptr || L->workspace_bytes < need) return DR_EINVAL;
-        a.counters = reinterpret_cast<uint32_t*>(L->workspace);
-        a.wpart = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(L->workspace) + (((int64_t)tiles * 4 + 255) / 256 * 256));
+        bind_split(a, L->workspace);
     }
     hipStream_t st = S(L->stream);
     const size_t ysz = a.y_f32 ? 4 : 2;
@@ -1929,6 +1951,7 @@ int prepare_moe(const dr_launch* L, const dr_moe* M, MoeArgs& a, int& pw, int& t
         a.seg[0].pstride = (unsigned)((ekp / kblk(DR_BFP4)) * 1024);
         if (ekp % a.kch) plan_chunks(a.k_pad, 256, &a.chunks, &a.kch, &a.waves, &a.splits, &a.cps);  // (a chunk in one unit)
     }
+    limit_splits(a);
     if (!rows)
         mr = 1;
     else if (L->m <= 2)
@@ -1957,8 +1980,7 @@ int dr_moe_matmul(const dr_launch* L, const dr_moe* M) {
     const int64_t need = workspace_bytes(a, pw, mr);
     if (need > 0) {
         if (L->workspace == nullptr || L->workspace_bytes < need) return DR_EINVAL;
-        a.counters = reinterpret_cast<uint32_t*>(L->workspace);
-        a.wpart = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(L->workspace) + (((int64_t)tiles * 4 + 255) / 256 * 256));
+        bind_split(a, L->workspace);
     }
     hipStream_t st = S(L->stream);
     const size_t ysz = a.y_f32 ? 4 : 2;

@@ -253,7 +253,10 @@ struct WaveBest {
 // one merges every slice's list and resets the counter. select_row returns true in the workgroup that holds the row's
 // final list (in wavefront 0's lanes, the largest in lane 0) and the count of the row's candidates.
 
-constexpr int SEL_T = 256;                   // threads a workgroup
+#ifndef DR_SEL_T
+#define DR_SEL_T 256
+#endif
+constexpr int SEL_T = DR_SEL_T;              // threads a workgroup
 constexpr int SEL_W = SEL_T / 64;            // wavefronts
 constexpr int SEL_SLICES = 64;               // workgroups a row at most
 
@@ -265,8 +268,9 @@ struct SelArgs {
     uint32_t* counts;           // [rows][slices]: each slice's candidate count (slices > 1)
 };
 
-// a row's arrival counter has a 256-byte line of its own (the rows' atomics do not queue behind each other), at a
-// place that depends on nothing but the row: a workspace reused for calls of other shapes keeps its counters at zero
+// a row's arrival counter has a 256-byte line of its own (the rows' atomics do not queue behind each other), in a
+// region of fixed size at the workspace's start: the lists and counts of a launch of any shape lie after it, so a
+// workspace shared by launches of any shape never finds an earlier launch's lists where a counter should be zero
 constexpr int SEL_CSTRIDE = 64;
 constexpr int SEL_MAXROWS = 32;  // the rows of a record (dr_topk's limit)
 constexpr int64_t SEL_COUNTER_BYTES = (int64_t)SEL_MAXROWS * SEL_CSTRIDE * 4;

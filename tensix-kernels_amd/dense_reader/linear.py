@@ -503,9 +503,10 @@ _WORKSPACE = {}
 
 
 def _workspace(device, stream, nbytes, kind="matmul"):
-    """The workspace of one kind of launch (the matmul's split K, or the top-k merge) on a device and stream: zeroed
-    once when allocated (or grown); every launch leaves its counters at zero, and launches on one stream never
-    overlap. The two kinds keep apart: each lays its counters out its own way."""
+    """The workspace of one kind of launch (the matmul's split K, or the top-k merge and head pick) on a device and
+    stream: zeroed once when allocated (or grown); every launch leaves its counters at zero, each kind's counters lie
+    at one place whatever the launch's shape, and launches on one stream never overlap. The two kinds keep apart: each
+    lays its counters out its own way."""
     key = (device, stream.cuda_stream, kind)
     ws = _WORKSPACE.get(key)
     if ws is None or ws.numel() < nbytes:

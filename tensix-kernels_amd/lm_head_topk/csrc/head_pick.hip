@@ -101,13 +101,13 @@ __global__ __launch_bounds__(SEL_T) void dr_pick_k(SelArgs A, uint32_t vocab, in
     // 2. the candidates' logits: x[r] . head[id], one wavefront a candidate, float32 in a fixed order (lane l sums
     // d = 8 l + 512 i + j, i then j ascending; then the lanes, a butterfly). A wavefront takes RG candidates at once
     // (j, j + SEL_W, ...) and issues every load of a span of DSPAN values for all of them before the first is used.
-    constexpr int DSPAN = 8 * 512, RG = 4;
+    constexpr int DSPAN = 8 * 512, RG = MAXTOP / SEL_W < 4 ? MAXTOP / SEL_W : 4;
     const uint16_t* xr = x + (size_t)r * ldx;
     for (int j0 = wave; j0 < n; j0 += RG * SEL_W) {
         const uint16_t* hr[RG];
 #pragma unroll
-        for (int t = 0; t < RG; ++t)  // (past n: candidate n - 1 again, its sum not kept)
-            hr[t] = head + (size_t)cid[min(j0 + t * SEL_W, n - 1)] * (size_t)ld_head;
+        for (int t = 0; t < RG; ++t)  // (past n: candidate j0's row again, its sum not kept)
+            hr[t] = head + (size_t)cid[j0 + t * SEL_W < n ? j0 + t * SEL_W : j0] * (size_t)ld_head;
         float acc[RG];
 #pragma unroll
         for (int t = 0; t < RG; ++t) acc[t] = 0.f;

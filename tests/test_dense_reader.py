@@ -345,6 +345,19 @@ def test_split_k(device, fmt):
             same(f"{fmt} K {k} rows {m} block list second block", host(one, m, 640)[:, 384:], host(two, m, 640)[:, 384:])
 
 
+def test_split_k_shapes_share_workspace(device):
+    """Split-K launches of any shape share one workspace: many tiles after few (with counters placed by the tile count,
+    the second launch's would lie where the first one's partial sums were), and back, each against the oracle."""
+    k = 9216
+    for n in (320, 4096, 320):
+        wt = matrix(n, k, 90 + n % 7)
+        tw, _ = linear.native_weight(device, wt, linear.bfloat8_b)
+        for m in (1, 3):
+            x, tx = x_input(device, m, k, 91 + m)
+            y = linear.matmul(tx, tw, None)
+            check(f"split K N {n} rows {m} after other shapes", host(y, m, n), ref(x, held(tw, n)))
+
+
 def test_pack_cache(device, tmp_path):
     """native_weight_cached: the first call packs and writes the cache, the second reads it back; the weights are
     byte for byte the same and the matmul bit for bit; another weight's call is refused until rebuild."""

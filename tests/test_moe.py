@@ -362,6 +362,43 @@ def test_pack_cache(device):
         shutil.rmtree(tmp, ignore_errors=True)
 
 
+def test_split_k_decode_loop(device):
+    """gate_up and down of an H = I = 2880 layer, both split K (their workgroups meet in one shared workspace), in a
+    decode loop of three steps on other experts and another x each: every step's h and y equal the same step run on a
+    fresh workspace, bit for bit (down's partial sums never land where gate_up's counters are), and the first step's
+    h the oracle's."""
+    Hb = Ib = 2880
+    Eb = 8
+    g = torch.Generator().manual_seed(30)
+    gu = (torch.randn(Eb, Hb, 2 * Ib, generator=g) * 0.02).to(BF)
+    dn = (torch.randn(Eb, Ib, Hb, generator=g) * 0.02).to(BF)
+    P = moe8.pack(device, gu, dn)
+    steps = []
+    for s in range(3):
+        ids = torch.randperm(Eb, generator=g)[:K]
+        wts = torch.softmax(torch.randn(K, generator=g), 0).to(BF)
+        x = torch.randn(1, Hb, generator=g).to(BF)
+        steps.append((ids, wts, x, ids.to(torch.int16).reshape(1, 1, 1, K).to(device.torch),
+                      wts.reshape(1, 1, 1, K).to(device.torch), x.reshape(1, 1, 1, Hb).to(device.torch)))
+
+    def step(st):
+        th = moe8.gate_up(st[5], P, st[3], st[4], K)
+        ty = moe8.down(th, P, st[3], K)
+        return host(th, K * Ib)[:1], host(ty, Hb)[:1]
+
+    loop = [step(st) for st in steps]
+    for i, st in enumerate(steps):
+        linear._WORKSPACE.clear()
+        h, y = step(st)
+        same(f"decode loop step {i}: h against the step alone", loop[i][0], h)
+        same(f"decode loop step {i}: y against the step alone", loop[i][1], y)
+    ids, wts, x = steps[0][:3]
+    held_gu = torch.stack([torch.from_numpy(O.held(gu[e].float(), "bfp4")) for e in ids.tolist()])
+    _, rh = MO.layer(x.float().numpy()[0], held_gu.double().numpy(), torch.zeros(K, Ib, 1).double().numpy(),
+                     list(range(K)), wts.float().numpy(), "silu")
+    check("decode loop step 0: h against the oracle", loop[0][0], torch.from_numpy(rh).reshape(1, -1), rel=REL)
+
+
 def test_graph_replay(device):
     """route, gate_up and down captured in one HIP graph, replayed several times with eager work between, equal the
     eager calls each time."""

@@ -370,8 +370,7 @@ __device__ __forceinline__ void chunk_int4(const Args& a, const uint8_t* const* 
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
             float v = bf16_to_f32(xp[u][m] & 0xFFFFu) + bf16_to_f32(xp[u][m] >> 16);
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o);
+            v = wsel::add_xor<8>(wsel::add_xor<4>(wsel::add_xor<2>(wsel::add_xor<1>(v))));  // (over the 16 lanes)
             rs[m] = 136.f * v;
 #pragma unroll
             for (int q = 0; q < PW; ++q) xs[q][m] = xp[u][m];
@@ -806,9 +805,8 @@ __global__ __launch_bounds__(512) void dr_gemv(const Args a) {
             for (int q = 0; q < PW; ++q)
 #pragma unroll
                 for (int m = 0; m < MR; ++m) {
-                    float v = sx[q][m];
-#pragma unroll
-                    for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o);
+                    float v = wsel::add_xor<8>(wsel::add_xor<4>(wsel::add_xor<2>(wsel::add_xor<1>(sx[q][m]))));
+                    v = wsel::add_xor<32>(wsel::add_xor<16>(v));
                     corr[q][m] = 136.f * v;
                 }
         } else {
@@ -820,8 +818,7 @@ __global__ __launch_bounds__(512) void dr_gemv(const Args a) {
 #pragma unroll
             for (int m = 0; m < MR; ++m) {
                 float v = acc[q][m];
-                v += __shfl_xor(v, 16);
-                v += __shfl_xor(v, 32);
+                v = wsel::add_xor<32>(wsel::add_xor<16>(v));
                 wsum[q][m] += v - corr[q][m];
             }
     }
@@ -900,12 +897,10 @@ __global__ __launch_bounds__(512) void dr_gemv_moe(const MoeArgs a) {
         for (int q = 0; q < PW; ++q)
 #pragma unroll
             for (int m = 0; m < MR; ++m) {
-                float c = sx[q][m];
-#pragma unroll
-                for (int o = 1; o < 64; o <<= 1) c += __shfl_xor(c, o);
+                float c = wsel::add_xor<8>(wsel::add_xor<4>(wsel::add_xor<2>(wsel::add_xor<1>(sx[q][m]))));
+                c = wsel::add_xor<32>(wsel::add_xor<16>(c));
                 float v = acc[q][m];
-                v += __shfl_xor(v, 16);
-                v += __shfl_xor(v, 32);
+                v = wsel::add_xor<32>(wsel::add_xor<16>(v));
                 wsum[q][m] += v - 136.f * c;
             }
     };

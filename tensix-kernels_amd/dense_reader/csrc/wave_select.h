@@ -69,6 +69,15 @@ __device__ __forceinline__ unsigned long long cmpx(unsigned long long v, bool la
     return ((b > a) == larger) ? b : a;
 }
 
+// v plus lane l ^ J's v: both lanes of a pair add the same two values, so they hold the same bits after, as after a
+// shuffle butterfly's step at that distance
+template <int J>
+__device__ __forceinline__ float add_xor(float v) {
+    uint32_t a, b;
+    xpair32<J>(__float_as_uint(v), a, b);
+    return __uint_as_float(a) + __uint_as_float(b);
+}
+
 // the sum of v over the wavefront, on every lane: a butterfly at distances 32, 16, ..., 1. Both lanes of a pair add
 // the same two values, so every lane ends with the same bits, in the order a shuffle butterfly would give.
 __device__ __forceinline__ float wave_sum_xor(float v) {

@@ -1505,14 +1505,17 @@ inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 int hip_status(hipError_t e) { return e == hipSuccess ? DR_OK : DR_EHIP; }
 
-// the K range of one chunk: 512 (two exponent groups) from K = 4096 up, else 256 (more wavefronts for small K)
+// the K range of one chunk: 512 (two exponent groups) from K = 2048 up, else 256 (at least four chunks, so four
+// wavefronts a tile)
 #ifndef DR_CHUNK_K
 #define DR_CHUNK_K 0
 #endif
 
-// a workgroup takes at most this many chunks; more K is split over several workgroups a tile
+// a workgroup takes at most this many chunks (its MAXW wavefronts two each); more K is split over several workgroups
+// a tile, which then meet in the workspace: fewer splits of more chunks beat more of fewer (K = 14336 at M = 8: 2 x 14
+// chunks 15.8 us, 4 x 7 17.7 us; the MoE down's K = 12288: 2 x 12 9.0 us, 3 x 8 9.9 us)
 #ifndef DR_SPLIT_CHUNKS
-#define DR_SPLIT_CHUNKS 8
+#define DR_SPLIT_CHUNKS 16
 #endif
 
 // the split of a padded K into chunks of ch
@@ -1526,7 +1529,7 @@ void plan_chunks(int k_pad, int ch, int* chunks, int* kch, int* waves, int* spli
 
 void plan(int k, int* chunks, int* kch, int* waves, int* splits, int* cps) {
     const int k_pad = (k + KALIGN - 1) / KALIGN * KALIGN;
-    plan_chunks(k_pad, DR_CHUNK_K ? DR_CHUNK_K : (k_pad >= 4096 ? 512 : 256), chunks, kch, waves, splits, cps);
+    plan_chunks(k_pad, DR_CHUNK_K ? DR_CHUNK_K : (k_pad >= 2048 ? 512 : 256), chunks, kch, waves, splits, cps);
 }
 
 // a launch of more tiles than the workspace has counters for runs unsplit

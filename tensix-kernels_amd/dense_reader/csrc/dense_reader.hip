@@ -1777,6 +1777,23 @@ int prepare(const dr_launch* L, Args& a, int& pw, int& tiles, int& mr) {
         tiles += d.tiles;
         if ((int64_t)s.col0 + d.n_out > L->ldy) return DR_EINVAL;
     }
+    // A block list's segments in order of the bytes a tile reads (bf16, then bfloat8_b, then bfloat4_b; stable): the
+    // lowest workgroup indices start first, so the heaviest tiles do not queue for a CU behind lighter ones (each
+    // segment keeps its own output columns; the order changes no result).
+    if (a.nseg > 1) {
+        auto heavier = [](int f, int g) { return (f == DR_BF16 ? 3 : f == DR_BFP8 ? 2 : 1) > (g == DR_BF16 ? 3 : g == DR_BFP8 ? 2 : 1); };
+        for (int i = 1; i < a.nseg; ++i) {
+            const SegDev v = a.seg[i];
+            int j = i - 1;
+            for (; j >= 0 && heavier(v.fmt, a.seg[j].fmt); --j) a.seg[j + 1] = a.seg[j];
+            a.seg[j + 1] = v;
+        }
+        int tb = 0;
+        for (int i = 0; i < a.nseg; ++i) {
+            a.seg[i].tile_begin = tb;
+            tb += a.seg[i].tiles;
+        }
+    }
     if (a.res != nullptr && (L->ldr < a.seg[0].col0 + a.seg[0].n_out || L->nseg != 1 || pw != 2)) return DR_EINVAL;
     const dr_topk& T = L->topk;
     a.rec = reinterpret_cast<uint32_t*>(T.records);

@@ -152,6 +152,18 @@ __device__ __forceinline__ void dot2_bcast(float& acc, uint32_t p, uint32_t a) {
                      : "+v"(acc) : "v"(p), "v"(a), "i"(J));
 }
 
+// After the last v_dot2c of a run of bfp4_step: every accumulator passes through an empty volatile asm. Volatile asm
+// statements keep their order, so no instruction that reads an accumulator can be scheduled before the last dot2c
+// and its s_nop 2 (the other accumulators' last dot2c lie at least four dot2c further back); without it the compiler
+// may hoist a reader of one accumulator between the dot2c of the others, inside the DOT result's wait states.
+template <int PW, int MR>
+__device__ __forceinline__ void dot_fence(float (&acc)[PW][MR]) {
+#pragma unroll
+    for (int q = 0; q < PW; ++q)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) asm volatile("" : "+v"(acc[q][m]));
+}
+
 // a value the compiler cannot see through: masks made with it keep a load unconditional (a known-zero mask lets the
 // compiler put the load under a branch, and a load under a branch waits for every load before it)
 __device__ __forceinline__ uint32_t opaque(uint32_t v) {
@@ -322,6 +334,7 @@ __device__ __forceinline__ void chunk_bfp4(const Args& a, const uint8_t* const* 
         }
         bfp4_step<0, MR, PW>(acc, xs, c[u].c);
     }
+    dot_fence(acc);
 }
 
 // int4 (W4A16): the bfloat4_b code layout with no exponents (every value q = u - 8) and a bf16 scale per column and 32
@@ -381,6 +394,7 @@ __device__ __forceinline__ void chunk_int4(const Args& a, const uint8_t* const* 
 #pragma unroll
             for (int m = 0; m < MR; ++m) t[q][m] = 0.f;
         bfp4_step<0, MR, PW>(t, xs, c[u].c);
+        dot_fence(t);
 #pragma unroll
         for (int q = 0; q < PW; ++q)
 #pragma unroll
@@ -436,6 +450,54 @@ __device__ __forceinline__ void chunk_bf16(const Args& a, const uint8_t* const* 
 __device__ __forceinline__ float load_scale(const void* s, int f32, int col) {
     if (s == nullptr) return 1.f;
     return f32 ? reinterpret_cast<const float*>(s)[col] : bf16_to_f32(reinterpret_cast<const uint16_t*>(s)[col]);
+}
+
+// The epilogue's operands from memory (column scales, residual), read before the K loop so that their latency hides
+// under it instead of adding to the workgroup's end: thread c < TILE the scales of the tile's output column c (gate
+// and up with a GLU), thread e the residual of its first epilogue element (row e / TILE, column e % TILE). After the K
+// loop they go to LDS (pre: [0, TILE) the scale or gate scale, [TILE, 2 TILE) the up scale, from PRE_RES the
+// residual by thread), where the epilogue takes them.
+constexpr int PRE_RES = 2 * TILE;
+constexpr int PRE_FLOATS = PRE_RES + 64 * MAXW;
+
+struct EpiPre {
+    float sg, su, res;
+};
+
+template <int ROWS, int PW>
+__device__ __forceinline__ EpiPre epi_prefetch(const Args& a, const SegDev& sg, int t) {
+    EpiPre p{1.f, 1.f, 0.f};
+    const int e = threadIdx.x;
+    if (e < TILE) {
+        const int oc = t * TILE + e;
+        if (oc < sg.n_out) {
+            if (PW == 4) {
+                if (sg.glu == 1) {
+                    p.sg = load_scale(sg.scale, sg.scale_f32, 2 * t * TILE + e);
+                    p.su = load_scale(sg.scale, sg.scale_f32, 2 * t * TILE + TILE + e);
+                } else {
+                    p.sg = load_scale(sg.scale, sg.scale_f32, oc);
+                    p.su = load_scale(sg.scale_up, sg.scale_f32, oc);
+                }
+            } else {
+                p.sg = load_scale(sg.scale, sg.scale_f32, oc);
+            }
+        }
+    }
+    if (PW == 2 && a.res != nullptr && e < ROWS * TILE) {
+        const int m = e / TILE, oc = t * TILE + e % TILE;
+        if (m < min(a.m, ROWS) && oc < sg.n_out) p.res = bf16_to_f32(a.res[(size_t)m * a.ldr + sg.col0 + oc]);
+    }
+    return p;
+}
+
+__device__ __forceinline__ void epi_stage(const EpiPre& p, float* pre) {
+    const int e = threadIdx.x;
+    if (e < TILE) {
+        pre[e] = p.sg;
+        pre[TILE + e] = p.su;
+    }
+    pre[PRE_RES + e] = p.res;
 }
 
 // the dense GLU's activation: silu(g) = g * sigmoid(g); gelu_tanh(g) = g * sigmoid(1.5957691216 g + 0.0713548162 g^3)
@@ -558,7 +620,8 @@ __device__ __forceinline__ void panel_ptrs(const SegDev& sg, int t, int k_pad, c
 // the tile for the top-k ranking.
 template <int ROWS, int PW>
 __device__ __forceinline__ void epilogue(const Args& a, const SegDev& sg, int t, const float* part, int nparts,
-                                         float (*tval)[TILE], uint32_t (*tkey)[TILE], int wave, int lane) {
+                                         float (*tval)[TILE], uint32_t (*tkey)[TILE], int wave, int lane,
+                                         const float* pre = nullptr) {
     const int mrows = min(a.m, ROWS);
     const bool topk = a.rec != nullptr;
     for (int e = threadIdx.x; e < TILE * ROWS; e += blockDim.x) {
@@ -575,7 +638,10 @@ __device__ __forceinline__ void epilogue(const Args& a, const SegDev& sg, int t,
             }
             float sgv = 1.f, suv = 1.f;
             if (valid) {
-                if (sg.glu == 1) {
+                if (pre != nullptr) {
+                    sgv = pre[col];
+                    suv = pre[TILE + col];
+                } else if (sg.glu == 1) {
                     sgv = load_scale(sg.scale, sg.scale_f32, 2 * t * TILE + col);
                     suv = load_scale(sg.scale, sg.scale_f32, 2 * t * TILE + TILE + col);
                 } else {
@@ -586,11 +652,15 @@ __device__ __forceinline__ void epilogue(const Args& a, const SegDev& sg, int t,
             v = act_glu(gsum * sgv, a.act) * (usum * suv);
         } else {
             const size_t ycol = (size_t)sg.col0 + oc;
-            if (valid && a.res != nullptr && a.res_mode == 2) v = bf16_to_f32(a.res[(size_t)m * a.ldr + ycol]);
+            // (the residual: prefetched for the thread's first element)
+            const bool rpre = pre != nullptr && e == (int)threadIdx.x;
+            float rv = 0.f;
+            if (valid && a.res != nullptr) rv = rpre ? pre[PRE_RES + e] : bf16_to_f32(a.res[(size_t)m * a.ldr + ycol]);
+            if (valid && a.res != nullptr && a.res_mode == 2) v = rv;
             for (int w = 0; w < nparts; ++w) v += part[((w * PW + cq) * ROWS + m) * 16 + cc];
             if (valid) {
-                v *= load_scale(sg.scale, sg.scale_f32, oc);
-                if (a.res != nullptr && a.res_mode == 1) v += bf16_to_f32(a.res[(size_t)m * a.ldr + ycol]);
+                v *= pre != nullptr ? pre[col] : load_scale(sg.scale, sg.scale_f32, oc);
+                if (a.res != nullptr && a.res_mode == 1) v += rv;
             }
         }
         float out = v;
@@ -773,6 +843,9 @@ __global__ __launch_bounds__(512) void dr_gemv(const Args a) {
     const uint8_t* eb[PW];
     panel_ptrs<PW>(sg, t, a.k_pad, cb, eb);
 
+    __shared__ float pre[PRE_FLOATS];
+    const EpiPre ep = epi_prefetch<MR, PW>(a, sg, t);
+
     float wsum[PW][MR];  // this wavefront's column sums (lanes 0..15), its chunks added in order
 #pragma unroll
     for (int q = 0; q < PW; ++q)
@@ -828,9 +901,10 @@ __global__ __launch_bounds__(512) void dr_gemv(const Args a) {
 #pragma unroll
             for (int m = 0; m < MR; ++m) part[((wave * PW + q) * MR + m) * 16 + lane] = wsum[q][m];
     }
+    epi_stage(ep, pre);
     __syncthreads();
     const int nparts = gather_splits<MR, PW>(a, g, split, part);
-    if (nparts) epilogue<MR, PW>(a, sg, t, part, nparts, tval, tkey, wave, lane);
+    if (nparts) epilogue<MR, PW>(a, sg, t, part, nparts, tval, tkey, wave, lane, pre);
 }
 
 
@@ -1171,6 +1245,8 @@ __global__ __launch_bounds__(512) void dr_mfma(const Args a) {
     const uint8_t* cb[PW];
     const uint8_t* eb[PW];
     panel_ptrs<PW>(sg, t, a.k_pad, cb, eb);
+    __shared__ float pre[PRE_FLOATS];
+    const EpiPre ep = epi_prefetch<ROWS, PW>(a, sg, t);
 
     f32x4 acc[PW][MT];  // this wavefront's sums over its chunks, in order
 #pragma unroll
@@ -1195,9 +1271,10 @@ __global__ __launch_bounds__(512) void dr_mfma(const Args a) {
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 part[((wave * PW + q) * ROWS + 16 * tt + 4 * (lane >> 4) + j) * 16 + (lane & 15)] = acc[q][tt][j];
+    epi_stage(ep, pre);
     __syncthreads();
     const int nparts = gather_splits<ROWS, PW>(a, g, split, part);
-    if (nparts) epilogue<ROWS, PW>(a, sg, t, part, nparts, tval, tkey, wave, lane);
+    if (nparts) epilogue<ROWS, PW>(a, sg, t, part, nparts, tval, tkey, wave, lane, pre);
 }
 
 template <int MT, int PW, int MOE>

@@ -25,6 +25,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <stdint.h>
 
 #include "dense_reader.h"
@@ -40,6 +41,12 @@ namespace {
 constexpr int KALIGN = 256;  // K padding: one exponent group; a multiple of every format's k-block
 constexpr int MAXW = 8;      // wavefronts a workgroup at most (512 threads: up to 256 VGPRs a lane)
 constexpr int TILE = 32;
+
+// output columns of a workgroup's tile: 16 (one panel) for a narrow launch (PW = 1), else 32
+template <int PW>
+__host__ __device__ constexpr int tile_w() {
+    return PW == 1 ? 16 : TILE;
+}
 
 __host__ __device__ constexpr int kblk(int fmt) {
     return fmt == DR_BFP8 ? 64 : (fmt == DR_BFP4 || fmt == DR_INT4) ? 128 : 32;
@@ -453,10 +460,10 @@ __device__ __forceinline__ float load_scale(const void* s, int f32, int col) {
 }
 
 // The epilogue's operands from memory (column scales, residual), read before the K loop so that their latency hides
-// under it instead of adding to the workgroup's end: thread c < TILE the scales of the tile's output column c (gate
-// and up with a GLU), thread e the residual of its first epilogue element (row e / TILE, column e % TILE). After the K
-// loop they go to LDS (pre: [0, TILE) the scale or gate scale, [TILE, 2 TILE) the up scale, from PRE_RES the
-// residual by thread), where the epilogue takes them.
+// under it instead of adding to the workgroup's end: thread c < TW (the tile's width) the scales of the tile's output
+// column c (gate and up with a GLU), thread e the residual of its first epilogue element (row e / TW, column e % TW).
+// After the K loop they go to LDS (pre: [0, TILE) the scale or gate scale, [TILE, 2 TILE) the up scale, from PRE_RES
+// the residual by thread), where the epilogue takes them.
 constexpr int PRE_RES = 2 * TILE;
 constexpr int PRE_FLOATS = PRE_RES + 64 * MAXW;
 
@@ -466,10 +473,11 @@ struct EpiPre {
 
 template <int ROWS, int PW>
 __device__ __forceinline__ EpiPre epi_prefetch(const Args& a, const SegDev& sg, int t) {
+    constexpr int TW = tile_w<PW>();
     EpiPre p{1.f, 1.f, 0.f};
     const int e = threadIdx.x;
-    if (e < TILE) {
-        const int oc = t * TILE + e;
+    if (e < TW) {
+        const int oc = t * TW + e;
         if (oc < sg.n_out) {
             if (PW == 4) {
                 if (sg.glu == 1) {
@@ -484,8 +492,8 @@ __device__ __forceinline__ EpiPre epi_prefetch(const Args& a, const SegDev& sg, 
             }
         }
     }
-    if (PW == 2 && a.res != nullptr && e < ROWS * TILE) {
-        const int m = e / TILE, oc = t * TILE + e % TILE;
+    if (PW <= 2 && a.res != nullptr && e < ROWS * TW) {
+        const int m = e / TW, oc = t * TW + e % TW;
         if (m < min(a.m, ROWS) && oc < sg.n_out) p.res = bf16_to_f32(a.res[(size_t)m * a.ldr + sg.col0 + oc]);
     }
     return p;
@@ -597,8 +605,8 @@ __device__ __forceinline__ void panel_ptrs(const SegDev& sg, int t, int k_pad, c
         int p;
         const uint8_t* cbase = sg.codes;
         const uint8_t* ebase = sg.exps;
-        if (PW == 2) {
-            p = 2 * t + q;
+        if (PW <= 2) {
+            p = PW * t + q;  // (a narrow launch: the tile is one panel)
         } else if (sg.glu == 1) {
             p = 4 * t + q;  // interleave_glu: gate tile 2t, up tile 2t + 1
         } else {
@@ -622,11 +630,12 @@ template <int ROWS, int PW>
 __device__ __forceinline__ void epilogue(const Args& a, const SegDev& sg, int t, const float* part, int nparts,
                                          float (*tval)[TILE], uint32_t (*tkey)[TILE], int wave, int lane,
                                          const float* pre = nullptr) {
+    constexpr int TW = tile_w<PW>();
     const int mrows = min(a.m, ROWS);
-    const bool topk = a.rec != nullptr;
-    for (int e = threadIdx.x; e < TILE * ROWS; e += blockDim.x) {
-        const int m = e / TILE, col = e % TILE;
-        const int oc = t * TILE + col;  // output column of this segment
+    const bool topk = a.rec != nullptr;  // (never with PW = 1)
+    for (int e = threadIdx.x; e < TW * ROWS; e += blockDim.x) {
+        const int m = e / TW, col = e % TW;
+        const int oc = t * TW + col;  // output column of this segment
         const bool valid = m < mrows && oc < sg.n_out;
         float v = 0.f;
         const int cq = col >> 4, cc = col & 15;
@@ -864,7 +873,7 @@ __global__ __launch_bounds__(512) void dr_gemv(const Args a) {
         } else if (FMT == DR_INT4) {
             const uint16_t* gs[PW];
 #pragma unroll
-            for (int q = 0; q < PW; ++q) gs[q] = sg.gscale + (size_t)(2 * t + q) * (a.k_pad / 128) * 64;
+            for (int q = 0; q < PW; ++q) gs[q] = sg.gscale + (size_t)(PW * t + q) * (a.k_pad / 128) * 64;
             chunk_int4<MR, PW>(a, cb, gs, k0, k1, lane, acc);
         } else if (fmt == DR_BFP4) {
             float sx[PW][MR];
@@ -1582,6 +1591,19 @@ inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 int hip_status(hipError_t e) { return e == hipSuccess ? DR_OK : DR_EHIP; }
 
+// CUs of the current device (read once a device; 256 if it cannot be read)
+int cu_count() {
+    static std::atomic<int> cus[64];
+    int d = 0;
+    if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= 64) return 256;
+    int v = cus[d].load(std::memory_order_relaxed);
+    if (v == 0) {
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, d) != hipSuccess || v <= 0) v = 256;
+        cus[d].store(v, std::memory_order_relaxed);
+    }
+    return v;
+}
+
 // the K range of one chunk: 512 (two exponent groups) from K = 2048 up, else 256 (at least four chunks, so four
 // wavefronts a tile)
 #ifndef DR_CHUNK_K
@@ -1640,7 +1662,7 @@ void launch_gemv(const Args& a, int grid, hipStream_t st) {
         case DR_BFP8: hipLaunchKernelGGL((dr_gemv<MR, PW, DR_BFP8, true>), dim3(grid), b, lds, st, a); break;
         case DR_BFP4: hipLaunchKernelGGL((dr_gemv<MR, PW, DR_BFP4, true>), dim3(grid), b, lds, st, a); break;
         case DR_INT4:
-            if constexpr (PW == 2 && MR <= 2) hipLaunchKernelGGL((dr_gemv<MR, PW, DR_INT4, true>), dim3(grid), b, lds, st, a);
+            if constexpr (PW <= 2 && MR <= 2) hipLaunchKernelGGL((dr_gemv<MR, PW, DR_INT4, true>), dim3(grid), b, lds, st, a);
             break;
         default: hipLaunchKernelGGL((dr_gemv<MR, PW, DR_BF16, true>), dim3(grid), b, lds, st, a); break;
     }
@@ -1706,8 +1728,8 @@ hipError_t launch_moe(const MoeArgs& a, int mode, int rows, int grid, hipStream_
 // one pass of up to `rows` rows
 hipError_t launch_rows(const Args& a, int rows, int pw, int grid, hipStream_t st) {
     switch (rows) {
-        case 1: pw == 2 ? launch_gemv<1, 2>(a, grid, st) : launch_gemv<1, 4>(a, grid, st); break;
-        case 2: pw == 2 ? launch_gemv<2, 2>(a, grid, st) : launch_gemv<2, 4>(a, grid, st); break;
+        case 1: pw == 1 ? launch_gemv<1, 1>(a, grid, st) : pw == 2 ? launch_gemv<1, 2>(a, grid, st) : launch_gemv<1, 4>(a, grid, st); break;
+        case 2: pw == 1 ? launch_gemv<2, 1>(a, grid, st) : pw == 2 ? launch_gemv<2, 2>(a, grid, st) : launch_gemv<2, 4>(a, grid, st); break;
         case 4: pw == 2 ? launch_gemv<4, 2>(a, grid, st) : launch_gemv<4, 4>(a, grid, st); break;
         case 8: launch_gemv<8, 2>(a, grid, st); break;  // (a GLU pass takes at most 4 GEMV rows)
         case 16: pw == 2 ? launch_mfma<1, 2>(a, grid, st) : launch_mfma<1, 4>(a, grid, st); break;
@@ -1802,7 +1824,7 @@ int dr_plan(int k, int m, int32_t* chunks, int32_t* kch, int32_t* rpp) {
 namespace {
 
 // the launch's arguments, its panel width, tiles and rows a pass (shared by dr_matmul and dr_workspace_bytes)
-int prepare(const dr_launch* L, Args& a, int& pw, int& tiles, int& mr) {
+int prepare(const dr_launch* L, Args& a, int& pw, int& tiles, int& mr, bool narrow_ok = true) {
     if (L == nullptr || L->x == nullptr || L->y == nullptr || L->m <= 0 || L->k <= 0 || L->k % 32 ||
         L->ldx < L->k || L->nseg < 1 || L->nseg > 4)
         return DR_EINVAL;
@@ -1893,6 +1915,21 @@ int prepare(const dr_launch* L, Args& a, int& pw, int& tiles, int& mr) {
     if (pw == 4 && mr == 8) mr = 4;    // (GLU: at most 4 GEMV rows or 16 MFMA rows a pass, for the registers
     if (pw == 4 && mr == 32) mr = 16;  // and the LDS)
     if (a.seg[0].fmt == DR_INT4) mr = L->m >= 2 ? 2 : 1;  // (int4: the GEMV, two rows a pass)
+    // A GEMV launch of fewer 32-column tiles than the device has CUs takes 16-column tiles (one panel a workgroup),
+    // so every CU streams: each column's sums are made by the same lanes in the same order whatever the tile width,
+    // so the results are the same bit for bit. (Not with top-k records, one a 32-column tile, nor a GLU's pairs.)
+    if (narrow_ok && pw == 2 && mr <= 2 && a.rec == nullptr && tiles < cu_count()) {
+        pw = 1;
+        tiles = 0;
+        for (int i = 0; i < a.nseg; ++i) {
+            a.seg[i].tiles = (a.seg[i].n_out + 15) / 16;
+            a.seg[i].tile_begin = tiles;
+            tiles += a.seg[i].tiles;
+        }
+        a.tiles = tiles;
+        plan(L->k, &a.chunks, &a.kch, &a.waves, &a.splits, &a.cps);
+        limit_splits(a);
+    }
     return DR_OK;
 }
 
@@ -2017,7 +2054,7 @@ int prepare_moe(const dr_launch* L, const dr_moe* M, MoeArgs& a, int& pw, int& t
         B.k = units * ekp;  // (the gathered K, each unit's block padded)
         B.ldx = std::max(L->ldx, B.k);
     }
-    const int st = prepare(&B, a, pw, tiles, mr);
+    const int st = prepare(&B, a, pw, tiles, mr, false);
     if (st != DR_OK) return st;
     a.ldx = L->ldx;
     a.ids = M->ids;

@@ -214,6 +214,26 @@ def test_block_list_bitwise(device):
         )
 
 
+@pytest.mark.parametrize("fmt", ["bfp8", "bfp4", "bf16"])
+def test_narrow_tiles_bitwise(device, fmt):
+    """A launch of fewer 32-column tiles than the device has CUs runs 16-column tiles: the same columns inside a launch
+    of many tiles (a block list with a wide second block, 32-column tiles) are the same bit for bit, with scales and a
+    split K."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    for k in (2048, 9216):
+        n = 1000
+        tw, _ = linear.native_weight(device, matrix(n, k, 80), DTYPES[fmt])
+        big, _ = linear.native_weight(device, matrix(32 * cus, k, 81), DTYPES[fmt])
+        sc = linear.scale_tensor(device, torch.rand(n, generator=torch.Generator().manual_seed(82)) + 0.5,
+                                 dtype=linear.float32)
+        for m in (1, 2):
+            x, tx = x_input(device, m, k, 83 + m)
+            alone = host(linear.matmul(tx, tw, sc), m, n)
+            check(f"{fmt} K {k} rows {m} narrow tiles", alone, ref(x, held(tw, n)) * sc.float().cpu().reshape(1, -1))
+            wide = linear.matmul(tx, [(tw, 0, sc), (big, 32)], None)
+            same(f"{fmt} K {k} rows {m} narrow against wide tiles", host(wide, m, n), alone)
+
+
 def test_max_banks(device):
     k, n, m = 1024, 1024, 2
     banks = cdev.dram_banks(device)

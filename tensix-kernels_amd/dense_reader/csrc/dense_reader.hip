@@ -597,7 +597,8 @@ __device__ __forceinline__ int find_segment(const Args& a, int g) {
 
 // the code and exponent bases of the tile's PW panels: plain weights the tile's two panels; interleave_glu weights the
 // gate tile's two panels then the up tile's; gate and up weights apart their tile's two panels each
-template <int PW>
+// GU (the expert gather's gate/up launches, gate and up apart): PW = 2 is a 16-column tile's gate panel and up panel.
+template <int PW, bool GU = false>
 __device__ __forceinline__ void panel_ptrs(const SegDev& sg, int t, int k_pad, const uint8_t* (&cb)[PW],
                                            const uint8_t* (&eb)[PW]) {
 #pragma unroll
@@ -605,7 +606,13 @@ __device__ __forceinline__ void panel_ptrs(const SegDev& sg, int t, int k_pad, c
         int p;
         const uint8_t* cbase = sg.codes;
         const uint8_t* ebase = sg.exps;
-        if (PW <= 2) {
+        if (GU && PW == 2) {
+            p = t;
+            if (q == 1) {
+                cbase = sg.codes_up;
+                ebase = sg.exps_up;
+            }
+        } else if (PW <= 2) {
             p = PW * t + q;  // (a narrow launch: the tile is one panel)
         } else if (sg.glu == 1) {
             p = 4 * t + q;  // interleave_glu: gate tile 2t, up tile 2t + 1
@@ -724,10 +731,11 @@ __device__ __forceinline__ void epilogue(const Args& a, const SegDev& sg, int t,
 
 // the gate/up modes' epilogue: thread (m, col) of the tile adds the bias, applies the GLU and the row's routing weight
 // for the expert (the slot's in DR_MOE_GATE_UP; 0 where the row did not choose it in DR_MOE_GATE_UP_ROWS) and writes
-// the unit's columns of y (moe_gu_compute.cpp: the GLU in dest, then times the weight's tile)
-template <int ROWS, int MOE>
+// the unit's columns of y (moe_gu_compute.cpp: the GLU in dest, then times the weight's tile). The tile is PW / 2 gate
+// panels then as many up panels: 32 columns, or 16 in a narrow launch (PW = 2).
+template <int ROWS, int PW, int MOE>
 __device__ __forceinline__ void epilogue_moe(const MoeArgs& a, int t, int unit, int ex, const float* part, int nparts) {
-    constexpr int PW = 4;
+    constexpr int TW = 8 * PW, H = PW / 2;
     __shared__ float coef[ROWS];
     const int mrows = min(a.m, ROWS);
     if (threadIdx.x < ROWS) {
@@ -744,15 +752,15 @@ __device__ __forceinline__ void epilogue_moe(const MoeArgs& a, int t, int unit, 
         coef[m] = c;
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < TILE * ROWS; e += blockDim.x) {
-        const int m = e / TILE, col = e % TILE;
-        const int oc = t * TILE + col;  // the column within the expert's
+    for (int e = threadIdx.x; e < TW * ROWS; e += blockDim.x) {
+        const int m = e / TW, col = e % TW;
+        const int oc = t * TW + col;  // the column within the expert's
         if (m >= mrows || oc >= a.en) continue;
         const int cq = col >> 4, cc = col & 15;
         float gsum = 0.f, usum = 0.f;
         for (int w = 0; w < nparts; ++w) {
             gsum += part[((w * PW + cq) * ROWS + m) * 16 + cc];
-            usum += part[((w * PW + 2 + cq) * ROWS + m) * 16 + cc];
+            usum += part[((w * PW + H + cq) * ROWS + m) * 16 + cc];
         }
         if (a.bias != nullptr) {
             gsum += bf16_to_f32(a.bias[((size_t)ex * 2 + 0) * a.en + oc]);
@@ -764,9 +772,11 @@ __device__ __forceinline__ void epilogue_moe(const MoeArgs& a, int t, int unit, 
 }
 
 // DR_MOE_GATE_UP with an id past the experts: the slot's columns of this tile are zeros
+template <int PW>
 __device__ __forceinline__ void moe_zero(const MoeArgs& a, int t, int unit) {
-    for (int col = threadIdx.x; col < TILE; col += blockDim.x) {
-        const int oc = t * TILE + col;
+    constexpr int TW = 8 * PW;
+    for (int col = threadIdx.x; col < TW; col += blockDim.x) {
+        const int oc = t * TW + col;
         if (oc < a.en) reinterpret_cast<uint16_t*>(a.y)[(size_t)unit * a.en + oc] = 0;
     }
 }
@@ -947,13 +957,13 @@ __global__ __launch_bounds__(512) void dr_gemv_moe(const MoeArgs a) {
         ex = MOE == DR_MOE_GATE_UP ? moe_id(a, 0, unit) : (unit < ul->count ? (int)ul->list[unit] : -1);
         ex = __builtin_amdgcn_readfirstlane(ex);
         if (ex < 0) {
-            if (MOE == DR_MOE_GATE_UP && split == 0) moe_zero(a, t, unit);
+            if (MOE == DR_MOE_GATE_UP && split == 0) moe_zero<PW>(a, t, unit);
             return;
         }
     }
     const uint8_t* cb[PW];
     const uint8_t* eb[PW];
-    panel_ptrs<PW>(sg, t, moe_k<MOE>() ? a.ekp : a.k_pad, cb, eb);
+    panel_ptrs<PW, moe_n<MOE>()>(sg, t, moe_k<MOE>() ? a.ekp : a.k_pad, cb, eb);
     if constexpr (moe_n<MOE>()) {
 #pragma unroll
         for (int q = 0; q < PW; ++q) {
@@ -1021,7 +1031,7 @@ __global__ __launch_bounds__(512) void dr_gemv_moe(const MoeArgs a) {
     const int nparts = gather_splits<MR, PW>(a, g, split, part);
     if (!nparts) return;
     if constexpr (moe_n<MOE>())
-        epilogue_moe<MR, MOE>(a, t, unit, ex, part, nparts);
+        epilogue_moe<MR, PW, MOE>(a, t, unit, ex, part, nparts);
     else
         epilogue<MR, PW>(a, sg, t, part, nparts, tval, tkey, wave, lane);
 }
@@ -1310,7 +1320,7 @@ __global__ __launch_bounds__(512) void dr_mfma_moe(const MoeArgs a) {
         ex = MOE == DR_MOE_GATE_UP ? moe_id(a, 0, unit) : (unit < ul->count ? (int)ul->list[unit] : -1);
         ex = __builtin_amdgcn_readfirstlane(ex);
         if (ex < 0) {
-            if (MOE == DR_MOE_GATE_UP && split == 0) moe_zero(a, t, unit);
+            if (MOE == DR_MOE_GATE_UP && split == 0) moe_zero<PW>(a, t, unit);
             return;
         }
     }
@@ -1368,7 +1378,7 @@ __global__ __launch_bounds__(512) void dr_mfma_moe(const MoeArgs a) {
     const int nparts = gather_splits<ROWS, PW>(a, g, split, part);
     if (!nparts) return;
     if constexpr (moe_n<MOE>())
-        epilogue_moe<ROWS, MOE>(a, t, unit, ex, part, nparts);
+        epilogue_moe<ROWS, PW, MOE>(a, t, unit, ex, part, nparts);
     else
         epilogue<ROWS, PW>(a, sg, t, part, nparts, tval, tkey, wave, lane);
 }
@@ -1604,6 +1614,14 @@ int cu_count() {
     return v;
 }
 
+// whether 16-column tiles lower the most that any CU streams against `tiles` 32-column ones: ceil(2 T / C) halves
+// against ceil(T / C) whole tiles (128 tiles: one half against one tile; 360: three halves against two tiles; 448:
+// four halves, two tiles, the same)
+bool narrow_better(int tiles) {
+    const int c = cu_count();
+    return (2 * tiles + c - 1) / c < 2 * ((tiles + c - 1) / c);
+}
+
 // the K range of one chunk: 512 (two exponent groups) from K = 2048 up, else 256 (at least four chunks, so four
 // wavefronts a tile)
 #ifndef DR_CHUNK_K
@@ -1699,15 +1717,20 @@ void launch_mfma_moe(const MoeArgs& a, int grid, hipStream_t st) {
 
 // one pass of an expert-gathered launch (bfloat4_b): the one-row modes on the GEMV; the rows modes on the GEMV up to
 // two rows, else the MFMA kernel (16 rows a pass for gate/up, 16 or 32 for down)
-hipError_t launch_moe(const MoeArgs& a, int mode, int rows, int grid, hipStream_t st) {
+hipError_t launch_moe(const MoeArgs& a, int mode, int rows, int pw, int grid, hipStream_t st) {
+    const bool narrow = pw == 2;  // (gate/up modes: 16-column tiles)
     switch (mode) {
-        case DR_MOE_GATE_UP: launch_gemv_moe<1, 4, DR_MOE_GATE_UP>(a, grid, st); break;
+        case DR_MOE_GATE_UP:
+            narrow ? launch_gemv_moe<1, 2, DR_MOE_GATE_UP>(a, grid, st) : launch_gemv_moe<1, 4, DR_MOE_GATE_UP>(a, grid, st);
+            break;
         case DR_MOE_DOWN: launch_gemv_moe<1, 2, DR_MOE_DOWN>(a, grid, st); break;
         case DR_MOE_GATE_UP_ROWS:
             if (rows == 1)
-                launch_gemv_moe<1, 4, DR_MOE_GATE_UP_ROWS>(a, grid, st);
+                narrow ? launch_gemv_moe<1, 2, DR_MOE_GATE_UP_ROWS>(a, grid, st)
+                       : launch_gemv_moe<1, 4, DR_MOE_GATE_UP_ROWS>(a, grid, st);
             else if (rows == 2)
-                launch_gemv_moe<2, 4, DR_MOE_GATE_UP_ROWS>(a, grid, st);
+                narrow ? launch_gemv_moe<2, 2, DR_MOE_GATE_UP_ROWS>(a, grid, st)
+                       : launch_gemv_moe<2, 4, DR_MOE_GATE_UP_ROWS>(a, grid, st);
             else
                 launch_mfma_moe<1, 4, DR_MOE_GATE_UP_ROWS>(a, grid, st);
             break;
@@ -1915,10 +1938,11 @@ int prepare(const dr_launch* L, Args& a, int& pw, int& tiles, int& mr, bool narr
     if (pw == 4 && mr == 8) mr = 4;    // (GLU: at most 4 GEMV rows or 16 MFMA rows a pass, for the registers
     if (pw == 4 && mr == 32) mr = 16;  // and the LDS)
     if (a.seg[0].fmt == DR_INT4) mr = L->m >= 2 ? 2 : 1;  // (int4: the GEMV, two rows a pass)
-    // A GEMV launch of fewer 32-column tiles than the device has CUs takes 16-column tiles (one panel a workgroup),
-    // so every CU streams: each column's sums are made by the same lanes in the same order whatever the tile width,
-    // so the results are the same bit for bit. (Not with top-k records, one a 32-column tile, nor a GLU's pairs.)
-    if (narrow_ok && pw == 2 && mr <= 2 && a.rec == nullptr && tiles < cu_count()) {
+    // A GEMV launch takes 16-column tiles (one panel a workgroup) where they lower the most any CU streams (fewer
+    // 32-column tiles than CUs, or a count just past a multiple of the CUs): each column's sums are made by the same
+    // lanes in the same order whatever the tile width, so the results are the same bit for bit. (Not with top-k
+    // records, one a 32-column tile, nor a GLU's pairs.)
+    if (narrow_ok && pw == 2 && mr <= 2 && a.rec == nullptr && narrow_better(tiles)) {
         pw = 1;
         tiles = 0;
         for (int i = 0; i < a.nseg; ++i) {
@@ -2068,9 +2092,20 @@ int prepare_moe(const dr_launch* L, const dr_moe* M, MoeArgs& a, int& pw, int& t
     a.cstride = M->codes_stride;
     a.estride = M->exps_stride;
     a.bias = reinterpret_cast<const uint16_t*>(M->bias);
+    if (!rows)
+        mr = 1;
+    else if (L->m <= 2)
+        mr = L->m;
+    else
+        mr = (nmode || L->m <= 16) ? 16 : 32;
     if (nmode) {
         a.en = M->expert_n;
         a.tpe = (a.en + TILE - 1) / TILE;
+        // the GEMV's 16-column tiles (a gate panel and an up panel) where they lower the most a CU streams
+        if (mr <= 2 && narrow_better(units * a.tpe)) {
+            pw = 2;
+            a.tpe = (a.en + 15) / 16;
+        }
         tiles = units * a.tpe;
         a.seg[0].tiles = tiles;
         a.tiles = tiles;
@@ -2081,12 +2116,6 @@ int prepare_moe(const dr_launch* L, const dr_moe* M, MoeArgs& a, int& pw, int& t
         if (ekp % a.kch) plan_chunks(a.k_pad, 256, &a.chunks, &a.kch, &a.waves, &a.splits, &a.cps);  // (a chunk in one unit)
     }
     limit_splits(a);
-    if (!rows)
-        mr = 1;
-    else if (L->m <= 2)
-        mr = L->m;
-    else
-        mr = (nmode || L->m <= 16) ? 16 : 32;
     return DR_OK;
 }
 
@@ -2119,7 +2148,7 @@ int dr_moe_matmul(const dr_launch* L, const dr_moe* M) {
         p.x = a.x + (size_t)r0 * a.ldx;
         p.y = reinterpret_cast<uint8_t*>(L->y) + (size_t)r0 * a.ldy * ysz;
         p.row0 = r0;
-        const hipError_t e = launch_moe(p, M->mode, mr, tiles * a.splits, st);
+        const hipError_t e = launch_moe(p, M->mode, mr, pw, tiles * a.splits, st);
         if (e != hipSuccess) return DR_EHIP;
     }
     return DR_OK;

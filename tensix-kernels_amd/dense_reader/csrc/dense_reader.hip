@@ -1718,12 +1718,14 @@ void launch_mfma_moe(const MoeArgs& a, int grid, hipStream_t st) {
 // one pass of an expert-gathered launch (bfloat4_b): the one-row modes on the GEMV; the rows modes on the GEMV up to
 // two rows, else the MFMA kernel (16 rows a pass for gate/up, 16 or 32 for down)
 hipError_t launch_moe(const MoeArgs& a, int mode, int rows, int pw, int grid, hipStream_t st) {
-    const bool narrow = pw == 2;  // (gate/up modes: 16-column tiles)
+    const bool narrow = pw == 2;  // (gate/up modes: 16-column tiles; down modes: pw 1)
     switch (mode) {
         case DR_MOE_GATE_UP:
             narrow ? launch_gemv_moe<1, 2, DR_MOE_GATE_UP>(a, grid, st) : launch_gemv_moe<1, 4, DR_MOE_GATE_UP>(a, grid, st);
             break;
-        case DR_MOE_DOWN: launch_gemv_moe<1, 2, DR_MOE_DOWN>(a, grid, st); break;
+        case DR_MOE_DOWN:
+            pw == 1 ? launch_gemv_moe<1, 1, DR_MOE_DOWN>(a, grid, st) : launch_gemv_moe<1, 2, DR_MOE_DOWN>(a, grid, st);
+            break;
         case DR_MOE_GATE_UP_ROWS:
             if (rows == 1)
                 narrow ? launch_gemv_moe<1, 2, DR_MOE_GATE_UP_ROWS>(a, grid, st)
@@ -1736,9 +1738,11 @@ hipError_t launch_moe(const MoeArgs& a, int mode, int rows, int pw, int grid, hi
             break;
         default:
             if (rows == 1)
-                launch_gemv_moe<1, 2, DR_MOE_DOWN_ROWS>(a, grid, st);
+                pw == 1 ? launch_gemv_moe<1, 1, DR_MOE_DOWN_ROWS>(a, grid, st)
+                        : launch_gemv_moe<1, 2, DR_MOE_DOWN_ROWS>(a, grid, st);
             else if (rows == 2)
-                launch_gemv_moe<2, 2, DR_MOE_DOWN_ROWS>(a, grid, st);
+                pw == 1 ? launch_gemv_moe<2, 1, DR_MOE_DOWN_ROWS>(a, grid, st)
+                        : launch_gemv_moe<2, 2, DR_MOE_DOWN_ROWS>(a, grid, st);
             else if (rows == 16)
                 launch_mfma_moe<1, 2, DR_MOE_DOWN_ROWS>(a, grid, st);
             else
@@ -2114,6 +2118,38 @@ int prepare_moe(const dr_launch* L, const dr_moe* M, MoeArgs& a, int& pw, int& t
         a.ekp = ekp;
         a.seg[0].pstride = (unsigned)((ekp / kblk(DR_BFP4)) * 1024);
         if (ekp % a.kch) plan_chunks(a.k_pad, 256, &a.chunks, &a.kch, &a.waves, &a.splits, &a.cps);  // (a chunk in one unit)
+        // The GEMV's tile width and K splits (the down modes have no block lists, so they may depend on N): the pair
+        // that lowers the most any CU streams, ceil(workgroups / CUs) workgroups of cps chunks x the width each; ties
+        // to fewer splits, then to 32 columns (the gpt-oss-shaped down, 90 tiles x 24 chunks: 16 columns in 4 splits of
+        // 6 chunks, 720 workgroups, against 32 columns in 2 splits, 180 workgroups on 256 CUs).
+        if (mr <= 2) {
+            const int c = cu_count(), t32 = a.seg[0].tiles, t16 = (a.seg[0].n_out + 15) / 16;
+            long best = -1;
+            int bw = 32, bcps = a.cps;
+            for (int s = 1; s <= 8 && s <= a.chunks; ++s) {
+                const int cps = (a.chunks + s - 1) / s, sp = (a.chunks + cps - 1) / cps;
+                for (int w = 16; w <= 32; w += 16) {
+                    const long wg = (long)(w == 16 ? t16 : t32) * sp;
+                    if ((w == 16 ? t16 : t32) > SPLIT_MAXTILES) continue;
+                    const long cost = (wg + c - 1) / c * cps * w;
+                    if (best < 0 || cost < best || (cost == best && (sp < (a.chunks + bcps - 1) / bcps ||
+                                                                     (sp == (a.chunks + bcps - 1) / bcps && w > bw)))) {
+                        best = cost;
+                        bw = w;
+                        bcps = cps;
+                    }
+                }
+            }
+            a.cps = bcps;
+            a.splits = (a.chunks + bcps - 1) / bcps;
+            a.waves = bcps < MAXW ? bcps : MAXW;
+            if (bw == 16) {
+                pw = 1;
+                tiles = t16;
+                a.seg[0].tiles = t16;
+                a.tiles = t16;
+            }
+        }
     }
     limit_splits(a);
     return DR_OK;

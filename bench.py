@@ -73,7 +73,8 @@ CONFIGS = {
     ),
     "moe": (
         "MoE layer decode, gpt-oss-20b shape: E=32 experts, top-4, H=2880, I=2880, swiglu_oai with gate/up bias, "
-        "bfp4 experts; a step is route (softmax top-4 of the router logits) + gate_up + down (moe8)",
+        "bfp4 experts; a step is route (softmax top-4 of the router logits) + gate_up, in one launch "
+        "(moe8.route_gate_up), then down",
         1,
         2880,
         [(2880, "bfp4", False)],
@@ -236,7 +237,8 @@ class Workload:
         if self.o.get("moe"):
             _, k, _, _ = self.moe_shape
             s_ = i % self.copies
-            self.moe8.gate_up(self.x, self.P, self.set_ids[s_], self.set_wts[s_], k, act="swiglu_oai")
+            self.moe8.route_gate_up(self.logits[s_], self.x, self.P, self.set_ids[s_], self.set_wts[s_], k,
+                                    act="swiglu_oai", loaders=2)
             return
         L, o, ws = self.linear, self.o, self.sets[i % self.copies]
         if o.get("glu2"):
@@ -263,8 +265,8 @@ class Workload:
     def step(self, i):
         if self.o.get("moe"):
             m8, (_, k, _, _) = self.moe8, self.moe_shape
-            m8.route(self.logits[i % self.copies], self.ids, self.wts, k)
-            h = m8.gate_up(self.x, self.P, self.ids, self.wts, k, act="swiglu_oai")
+            h = m8.route_gate_up(self.logits[i % self.copies], self.x, self.P, self.ids, self.wts, k,
+                                 act="swiglu_oai", loaders=2)
             m8.down(h, self.P, self.ids, k)
             return
         if self.o.get("lmhead"):
@@ -376,7 +378,7 @@ def main():
             "weight_bytes_per_call": wl.wbytes,
             "weight_copies_rotated": wl.copies,
             **({"experts": wl.moe_shape[0], "top_k": wl.moe_shape[1], "hidden": wl.moe_shape[2],
-                "intermediate": wl.moe_shape[3], "kernel": "gate_up (the step's larger launch)"}
+                "intermediate": wl.moe_shape[3], "kernel": "route_gate_up (the routing and gate_up in one launch, the step's larger)"}
                if wl.o.get("moe") else {}),
             "timing": "HIP graph of the timed steps, replayed; events on the replay stream",
         },

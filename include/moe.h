@@ -100,6 +100,15 @@ typedef struct dr_route {
 
 int dr_moe_route(const dr_route* route);
 
+/* dr_moe_route of one token (route->rows 1) and dr_moe_matmul's DR_MOE_GATE_UP over its picks, in one launch: every
+ * workgroup routes the token itself (the router's code: the same ids and weights bit for bit) and gathers its slot's
+ * expert; workgroup 0 writes ids and w as dr_moe_route does, for the down launch and the caller. route's ids, w,
+ * ids32 and experts are moe's; moe->slots is route->k (+ 1 with a slot); experts at most 256 (DR_ERANGE beyond: route
+ * with dr_moe_route, then dr_moe_matmul). The workspace is dr_moe_workspace_bytes(
+ * launch, moe)'s. Replaces the pair route (moe/moe8.py:1139-1253) then gate_up (moe/moe8.py:710-817): no kernel
+ * boundary between them. */
+int dr_moe_route_gate_up(const dr_launch* launch, const dr_moe* moe, const dr_route* route);
+
 #ifdef __cplusplus
 }
 #endif

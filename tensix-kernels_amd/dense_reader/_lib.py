@@ -35,6 +35,7 @@ SYMBOLS = (
     "dr_moe_workspace_bytes",
     "dr_moe_matmul",
     "dr_moe_route",
+    "dr_moe_route_gate_up",
 )
 
 DR_MOE_GATE_UP, DR_MOE_DOWN, DR_MOE_GATE_UP_ROWS, DR_MOE_DOWN_ROWS = 1, 2, 3, 4
@@ -194,6 +195,8 @@ def lib():
         L.dr_moe_matmul.argtypes = [ctypes.POINTER(Launch), ctypes.POINTER(Moe)]
         L.dr_moe_route.restype = c_int
         L.dr_moe_route.argtypes = [ctypes.POINTER(Route)]
+        L.dr_moe_route_gate_up.restype = c_int
+        L.dr_moe_route_gate_up.argtypes = [ctypes.POINTER(Launch), ctypes.POINTER(Moe), ctypes.POINTER(Route)]
         _lib = L
     return _lib
 

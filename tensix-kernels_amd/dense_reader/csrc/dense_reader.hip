@@ -30,6 +30,7 @@
 
 #include "dense_reader.h"
 #include "moe.h"
+#include "../../moe/csrc/moe_route.h"
 #include "wave_select.h"
 
 // No contraction of a multiply and an add into an FMA unless the code asks for one: the compiler would otherwise
@@ -119,7 +120,13 @@ struct MoeArgs : Args {
     int ek, ekp;         // down modes: an expert's rows (x's block width) and the rows packed (a multiple of 256)
     long long cstride, estride;  // bytes from one expert's codes / exponents to the next
     const uint16_t* bias;        // gate/up modes: [experts][2][en] bf16 (gate, up) or null
+    int routed;                  // DR_MOE_GATE_UP: every workgroup routes row 0 of route.logits itself (its ids and w
+    moe_route::RouteArgs route;  // are route's outputs, which workgroup 0 writes)
 };
+
+// the in-launch routing's experts a lane at most (E <= 256): the router's larger cases would raise the gather kernel's
+// registers for every launch
+constexpr int ROUTE_MAXPER = 4;
 
 // ---- the K loop of one wavefront: partial sums of PW panels x MR rows over [k0, k1) ------------------------------
 //
@@ -734,7 +741,8 @@ __device__ __forceinline__ void epilogue(const Args& a, const SegDev& sg, int t,
 // the unit's columns of y (moe_gu_compute.cpp: the GLU in dest, then times the weight's tile). The tile is PW / 2 gate
 // panels then as many up panels: 32 columns, or 16 in a narrow launch (PW = 2).
 template <int ROWS, int PW, int MOE>
-__device__ __forceinline__ void epilogue_moe(const MoeArgs& a, int t, int unit, int ex, const float* part, int nparts) {
+__device__ __forceinline__ void epilogue_moe(const MoeArgs& a, int t, int unit, int ex, const float* part, int nparts,
+                                             float wunit) {
     constexpr int TW = 8 * PW, H = PW / 2;
     __shared__ float coef[ROWS];
     const int mrows = min(a.m, ROWS);
@@ -743,7 +751,7 @@ __device__ __forceinline__ void epilogue_moe(const MoeArgs& a, int t, int unit, 
         float c = 0.f;
         if (m < mrows) {
             if (MOE == DR_MOE_GATE_UP) {
-                c = bf16_to_f32(a.rw[unit]);
+                c = wunit;  // (the slot's weight, read or routed at the workgroup's start)
             } else if (r < a.id_rows) {
                 for (int j = 0; j < a.slots; ++j)
                     if (moe_id(a, r, j) == ex) c = bf16_to_f32(a.rw[(size_t)r * a.ld_rw + j]);
@@ -951,10 +959,41 @@ __global__ __launch_bounds__(512) void dr_gemv_moe(const MoeArgs a) {
         moe_union(a, *ul);
     }
     int unit = 0, ex = 0;
+    float wunit = 0.f;  // DR_MOE_GATE_UP: the slot's routing weight
+    __shared__ int r_id[moe_route::MAXK];
+    __shared__ uint16_t r_w[moe_route::MAXK];
+    if constexpr (MOE == DR_MOE_GATE_UP) {
+        if (a.routed) {
+            // the token's routing, by wavefront 0 with the router's code (the same picks and weights bit for bit);
+            // the other wavefronts wait at the barrier. Workgroup 0 writes them out for the down launch and the caller.
+            __shared__ moe_route::RouteLds rl;
+            if (wave == 0) {
+                int mine;
+                uint16_t wbits;
+                moe_route::route_row<ROUTE_MAXPER>(a.route, 0, lane, rl, mine, wbits);
+                if (lane < a.route.k) {
+                    r_id[lane] = mine;
+                    r_w[lane] = wbits;
+                }
+                if (lane == 0 && a.route.slot >= 0) {  // (the slot column: its id at weight 1.0)
+                    r_id[a.route.k] = (int)a.route.slot;
+                    r_w[a.route.k] = 0x3F80u;
+                }
+                if (blockIdx.x == 0) moe_route::route_store(a.route, 0, lane, mine, wbits);
+            }
+            __syncthreads();
+        }
+    }
     if constexpr (moe_n<MOE>()) {
         unit = t / a.tpe;
         t -= unit * a.tpe;
-        ex = MOE == DR_MOE_GATE_UP ? moe_id(a, 0, unit) : (unit < ul->count ? (int)ul->list[unit] : -1);
+        if (MOE == DR_MOE_GATE_UP && a.routed) {
+            ex = r_id[unit] < a.experts ? r_id[unit] : -1;  // (as moe_id: an id past the experts chooses none)
+            wunit = bf16_to_f32(r_w[unit]);
+        } else {
+            ex = MOE == DR_MOE_GATE_UP ? moe_id(a, 0, unit) : (unit < ul->count ? (int)ul->list[unit] : -1);
+            if (MOE == DR_MOE_GATE_UP) wunit = bf16_to_f32(a.rw[unit]);
+        }
         ex = __builtin_amdgcn_readfirstlane(ex);
         if (ex < 0) {
             if (MOE == DR_MOE_GATE_UP && split == 0) moe_zero<PW>(a, t, unit);
@@ -1031,7 +1070,7 @@ __global__ __launch_bounds__(512) void dr_gemv_moe(const MoeArgs a) {
     const int nparts = gather_splits<MR, PW>(a, g, split, part);
     if (!nparts) return;
     if constexpr (moe_n<MOE>())
-        epilogue_moe<MR, PW, MOE>(a, t, unit, ex, part, nparts);
+        epilogue_moe<MR, PW, MOE>(a, t, unit, ex, part, nparts, wunit);
     else
         epilogue<MR, PW>(a, sg, t, part, nparts, tval, tkey, wave, lane);
 }
@@ -1378,7 +1417,7 @@ __global__ __launch_bounds__(512) void dr_mfma_moe(const MoeArgs a) {
     const int nparts = gather_splits<ROWS, PW>(a, g, split, part);
     if (!nparts) return;
     if constexpr (moe_n<MOE>())
-        epilogue_moe<ROWS, PW, MOE>(a, t, unit, ex, part, nparts);
+        epilogue_moe<ROWS, PW, MOE>(a, t, unit, ex, part, nparts, 0.f);
     else
         epilogue<ROWS, PW>(a, sg, t, part, nparts, tval, tkey, wave, lane);
 }
@@ -2188,6 +2227,30 @@ int dr_moe_matmul(const dr_launch* L, const dr_moe* M) {
         if (e != hipSuccess) return DR_EHIP;
     }
     return DR_OK;
+}
+
+int dr_moe_route_gate_up(const dr_launch* L, const dr_moe* M, const dr_route* R) {
+    moe_route::RouteArgs A;
+    const int sr = moe_route::route_args(R, A);
+    if (sr != DR_OK) return sr;
+    if (R->experts > 64 * ROUTE_MAXPER) return DR_ERANGE;  // (more experts: dr_moe_route, then dr_moe_matmul)
+    // one token routed into the buffers the gather then reads: the same ids, weights and experts
+    if (M == nullptr || M->mode != DR_MOE_GATE_UP || R->rows != 1 || R->ids != M->ids || R->w != M->w ||
+        (R->ids32 != 0) != (M->ids32 != 0) || R->experts != M->experts || M->slots != R->k + (R->slot >= 0 ? 1 : 0))
+        return DR_EINVAL;
+    MoeArgs a{};
+    int pw, tiles, mr;
+    const int st0 = prepare_moe(L, M, a, pw, tiles, mr);
+    if (st0 != DR_OK) return st0;
+    a.routed = 1;
+    a.route = A;
+    const int64_t need = workspace_bytes(a, pw, mr);
+    if (need > 0) {
+        if (L->workspace == nullptr || L->workspace_bytes < need) return DR_EINVAL;
+        bind_split(a, L->workspace);
+    }
+    const hipError_t e = launch_moe(a, M->mode, mr, pw, tiles * a.splits, S(L->stream));
+    return e == hipSuccess ? DR_OK : DR_EHIP;
 }
 
 }  // extern "C"

@@ -484,8 +484,9 @@ def _w_ptr(w, rows, k):
     return w.data_ptr(), ld
 
 
-def _run(P, x2, m, k_launch, ldx, y, ldy, gate_up_mode, mode, ids, ids32, w, slots, id_rows, act):
-    """One dr_moe_matmul: the launch of expert 0's weight and the gather (include/moe.h)."""
+def _run(P, x2, m, k_launch, ldx, y, ldy, gate_up_mode, mode, ids, ids32, w, slots, id_rows, act, route=None):
+    """One dr_moe_matmul: the launch of expert 0's weight and the gather (include/moe.h); with route (a dr_route),
+    dr_moe_route_gate_up: the token routed into ids and w by the same launch."""
     (gc, ge, dc, de), (gk, gn, dk, dn) = P["sizes"], P["pads"]
     L = _lib.Launch()
     L.x, L.m, L.k, L.ldx = x2.data_ptr(), m, k_launch, ldx
@@ -520,7 +521,10 @@ def _run(P, x2, m, k_launch, ldx, y, ldy, gate_up_mode, mode, ids, ids32, w, slo
     if need > 0:
         ws = linear._workspace(x2.device, stream, need)
         L.workspace, L.workspace_bytes = ws.data_ptr(), ws.numel()
-    _lib.check(lib.dr_moe_matmul(ctypes.byref(L), ctypes.byref(M)), "dr_moe_matmul")
+    if route is not None:
+        _lib.check(lib.dr_moe_route_gate_up(ctypes.byref(L), ctypes.byref(M), ctypes.byref(route)), "dr_moe_route_gate_up")
+    else:
+        _lib.check(lib.dr_moe_matmul(ctypes.byref(L), ctypes.byref(M)), "dr_moe_matmul")
     return y
 
 
@@ -600,19 +604,8 @@ def down_rows(h, P, ids, k, rows, *, ids32=False, kw=8, fidelity="hifi2", memory
 # --- the router ------------------------------------------------------------------------------------------------------
 
 
-def route(logits, ids, w, k, *, kind="softmax", bias=None, ids32=False, experts=None, shared=None, scale=1.0,
-          norm=True, groups=None, slot=None):
-    """The router's top k and their weights, written into ids [1, 1, R, k] (uint16, or uint32 with ids32) and w [1, 1,
-    R, k] bf16 (k + 1 slots with `slot`), slots in decreasing order of the pick's key, the lower id first among equal
-    keys. logits [1, 1, R, W] float32 on the GPU, R <= 32; experts (default W): its columns 0 .. E - 1, E a multiple of
-    32.
-    - kind "softmax": the top k by logit; the weights the softmax over the k.
-    - kind "sigmoid": the top k by sigmoid(logit) + bias (bias [E] float32, or None: by logit); the weights the picks'
-      sigmoids over their sum (norm=False: not divided).
-    shared: [1, 1, R, 1] bf16 that gets sigmoid(logits[:, E]). scale: every weight times it (0 < scale < 4). groups=
-    (n_group, topk_group) (sigmoid with a bias): a group's score the sum of its two largest keys, the topk_group best
-    groups kept (the lower group first among equal scores). slot: an id written as slot k of every row at weight 1.0.
-    Keys and weights in double, rounded to bf16 at the end. Returns w (reference moe8.py:1139-1253)."""
+def _route_args(logits, ids, w, k, kind, bias, ids32, experts, shared, scale, norm, groups, slot):
+    """route's arguments checked as route takes them, as a dr_route."""
     assert kind in ("softmax", "sigmoid"), f"moe8.route: kind {kind!r}"
     R, W = logits.shape[-2], logits.shape[-1]
     E = experts or W
@@ -646,8 +639,56 @@ def route(logits, ids, w, k, *, kind="softmax", bias=None, ids32=False, experts=
     A.n_group, A.topk_group = ng, tg
     A.slot = -1 if slot is None else int(slot)
     A.stream = torch.cuda.current_stream(logits.device).cuda_stream
+    return A
+
+
+
+
+def route(logits, ids, w, k, *, kind="softmax", bias=None, ids32=False, experts=None, shared=None, scale=1.0,
+          norm=True, groups=None, slot=None):
+    """The router's top k and their weights, written into ids [1, 1, R, k] (uint16, or uint32 with ids32) and w [1, 1,
+    R, k] bf16 (k + 1 slots with `slot`), slots in decreasing order of the pick's key, the lower id first among equal
+    keys. logits [1, 1, R, W] float32 on the GPU, R <= 32; experts (default W): its columns 0 .. E - 1, E a multiple of
+    32.
+    - kind "softmax": the top k by logit; the weights the softmax over the k.
+    - kind "sigmoid": the top k by sigmoid(logit) + bias (bias [E] float32, or None: by logit); the weights the picks'
+      sigmoids over their sum (norm=False: not divided).
+    shared: [1, 1, R, 1] bf16 that gets sigmoid(logits[:, E]). scale: every weight times it (0 < scale < 4). groups=
+    (n_group, topk_group) (sigmoid with a bias): a group's score the sum of its two largest keys, the topk_group best
+    groups kept (the lower group first among equal scores). slot: an id written as slot k of every row at weight 1.0.
+    Keys and weights in double, rounded to bf16 at the end. Returns w (reference moe8.py:1139-1253)."""
+    A = _route_args(logits, ids, w, k, kind, bias, ids32, experts, shared, scale, norm, groups, slot)
     _lib.check(_lib.lib().dr_moe_route(ctypes.byref(A)), "dr_moe_route")
     return w
+
+
+ROUTE_GATE_UP_MAX_E = 256  # (dr_moe_route_gate_up routes at most this many experts in the gather's launch)
+
+
+def route_gate_up(logits, x, P, ids, w, k, *, act="silu", kind="softmax", bias=None, ids32=False, shared=None,
+                  scale=1.0, norm=True, groups=None, slot=None, loaders=None, cpb=None):
+    """route(logits, ids, w, k, ...) of one token, then gate_up(x, P, ids, w, k + (slot given), act=act), in one
+    launch (dr_moe_route_gate_up): every workgroup of the gather routes the token itself, with the router's code, so
+    ids, w and h are route's and gate_up's bit for bit, with no kernel boundary between them. logits [1, 1, 1, W]
+    float32 (one row, E = P's experts); the other arguments as route's and gate_up's. More than 256 experts: route,
+    then gate_up (two launches, the same results). Returns h."""
+    assert logits.shape[-2] == 1 and logits.numel() == logits.shape[-1], tuple(logits.shape)
+    if P["E"] > ROUTE_GATE_UP_MAX_E:
+        route(logits, ids, w, k, kind=kind, bias=bias, ids32=ids32, experts=P["E"], shared=shared, scale=scale,
+              norm=norm, groups=groups, slot=slot)
+        return gate_up(x, P, ids, w, k + (slot is not None), ids32=ids32, loaders=loaders, cpb=cpb, act=act)
+    A = _route_args(logits, ids, w, k, kind, bias, ids32, P["E"], shared, scale, norm, groups, slot)
+    kk = k + (slot is not None)
+    assert act in ACTS, f"moe8: act {act!r}"
+    H, I = P["H"], P["I"]
+    _gu_cpb(P, cpb, GU_CPB)
+    split = _loaders(loaders, LOADERS)
+    G, _ = gu_groups(I // TILE, P["banks"])
+    assert G == 1 or split, "moe8: gate_up's column groups need two loaders (loaders=2)"
+    assert not P["gu_bias"] or split, "moe8: gate_up's bias needs two loaders (loaders=2)"
+    x2 = _x_rows(x, 1, H)[:1]
+    h = torch.empty(1, 1, 1, kk * I, dtype=torch.bfloat16, device=x2.device)
+    return _run(P, x2, 1, H, H, h, kk * I, True, _lib.DR_MOE_GATE_UP, ids, ids32, w, kk, 1, act, route=A)
 
 
 def route_reference(logits, k, kind="softmax", bias=None, scale=1.0, norm=True, groups=None, slot=None):

@@ -319,6 +319,71 @@ def test_route(device):
     )
 
 
+def test_route_gate_up_fused(device):
+    """route_gate_up (the token routed inside the gate/up launch) against route then gate_up: ids, weights, the shared
+    gate, h, and down's y on them bit for bit, over the router's options (softmax; uint32 ids; sigmoid with a bias and
+    a scale; groups; a slot inside and past the experts; a shared gate column), and replayed in a HIP graph."""
+    Ef, Hf, If = 64, 512, 256
+    g = torch.Generator().manual_seed(41)
+    gu = (torch.randn(Ef, Hf, 2 * If, generator=g) * 0.02).to(BF)
+    dn = (torch.randn(Ef, If, Hf, generator=g) * 0.02).to(BF)
+    gb = (torch.randn(Ef, 2 * If, generator=g) * 0.1).to(BF)
+    P = moe8.pack(device, gu, dn, gu_bias=gb)
+    x = torch.randn(1, 1, 1, Hf, generator=g).to(BF).to(device.torch)
+    bias = (torch.randn(Ef, generator=g) * 0.5).to(device.torch)
+    cases = [
+        ("softmax k 4", 4, {}),
+        ("softmax k 8 uint32", 8, {"ids32": True}),
+        ("sigmoid + bias k 6 scale 2.5", 6, {"kind": "sigmoid", "bias": bias, "scale": 2.5}),
+        ("sigmoid + bias groups 8/4 k 8", 8, {"kind": "sigmoid", "bias": bias, "groups": (8, 4)}),
+        ("softmax k 4 slot 5", 4, {"slot": 5}),
+        ("softmax k 3 slot past E", 3, {"slot": Ef + 3}),
+        ("softmax k 4 shared gate", 4, {"shared": True}),
+    ]
+    for name, k, opts in cases:
+        opts = dict(opts)
+        kk = k + ("slot" in opts)
+        idt = torch.int32 if opts.get("ids32") else torch.int16
+        width = Ef + (1 if opts.get("shared") else 0)
+        lg = (torch.randn(1, 1, 1, width, generator=g) * 2).to(device.torch)
+        lg[..., 7] = lg[..., 9]  # (a tie)
+        outs = []
+        for fused in (False, True):
+            ids = torch.full((1, 1, 1, kk), 1234, dtype=idt, device=device.torch)
+            w = torch.full((1, 1, 1, kk), float("nan"), dtype=BF, device=device.torch)
+            o = dict(opts)
+            sh = torch.zeros(1, 1, 1, 1, dtype=BF, device=device.torch) if o.pop("shared", False) else None
+            if fused:
+                h = moe8.route_gate_up(lg, x, P, ids, w, k, act="swiglu_oai", loaders=2, shared=sh, **o)
+            else:
+                moe8.route(lg, ids, w, k, experts=Ef, shared=sh, **o)
+                h = moe8.gate_up(x, P, ids, w, kk, act="swiglu_oai", loaders=2, ids32=o.get("ids32", False))
+            y = moe8.down(h, P, ids, kk, ids32=o.get("ids32", False))
+            outs.append([t.cpu() for t in (ids, w.view(torch.int16), h, y)] + ([sh.cpu()] if sh is not None else []))
+        for label, a, b in zip(("ids", "weights", "h", "y", "shared gate"), outs[0], outs[1]):
+            same(f"route_gate_up {name}: {label} against route then gate_up", b, a)
+    # a HIP graph of route_gate_up and down, replayed three times with eager work between, against the eager result
+    k = 4
+    lg = (torch.randn(1, 1, 1, Ef, generator=g) * 2).to(device.torch)
+    ids = torch.zeros(1, 1, 1, k, dtype=torch.int16, device=device.torch)
+    w = torch.zeros(1, 1, 1, k, dtype=BF, device=device.torch)
+    want_h = moe8.route_gate_up(lg, x, P, ids, w, k, act="silu", loaders=2)
+    want_y = moe8.down(want_h, P, ids, k).clone()
+    want_h = want_h.clone()
+    ids.zero_()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        gh = moe8.route_gate_up(lg, x, P, ids, w, k, act="silu", loaders=2)
+        gy = moe8.down(gh, P, ids, k)
+    for i in range(3):
+        ids.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        same(f"route_gate_up graph replay {i}: h", gh.cpu(), want_h.cpu())
+        same(f"route_gate_up graph replay {i}: y", gy.cpu(), want_y.cpu())
+
+
 def test_route_shared_gate(device):
     """shared: sigmoid of the logits' column E (a shared expert's gate folded into the router's matmul), in bf16."""
     g = torch.Generator().manual_seed(11)

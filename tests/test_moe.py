@@ -462,6 +462,10 @@ def test_split_k_decode_loop(device):
     _, rh = MO.layer(x.float().numpy()[0], held_gu.double().numpy(), torch.zeros(K, Ib, 1).double().numpy(),
                      list(range(K)), wts.float().numpy(), "silu")
     check("decode loop step 0: h against the oracle", loop[0][0], torch.from_numpy(rh).reshape(1, -1), rel=REL)
+    # down (16-column tiles in four K splits at this shape) on its own input: the step's bf16 h times the held rows
+    hd = loop[0][0].double().reshape(K, Ib)
+    ry = sum(hd[s] @ torch.from_numpy(O.held(dn[e].float(), "bfp4")).double() for s, e in enumerate(ids.tolist()))
+    check("decode loop step 0: y against the oracle on the step's h", loop[0][1], ry.reshape(1, -1).float(), rel=REL)
 
 
 def test_graph_replay(device):

@@ -100,6 +100,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--copy-probe", action="store_true")
+    ap.add_argument("--kblock", action="store_true",
+                    help="config moe: the experts packed with their shared exponents along K (moe8.pack(kblock=True))")
     return ap.parse_args()
 
 
@@ -132,8 +134,9 @@ class Workload:
     """The inputs of one config on the GPU and its two launch sequences: step(i) (the op as a user calls it) and
     kernel(i) (the matmul launch alone)."""
 
-    def __init__(self, name, linear, torch):
+    def __init__(self, name, linear, torch, kblock=False):
         self.name = name
+        self.kblock = kblock
         desc, m, k, ws, o = CONFIGS[name]
         self.desc, self.m, self.k, self.spec, self.o = desc, m, k, ws, o
         self.linear = linear
@@ -208,7 +211,7 @@ class Workload:
         gate_up = torch.randn(E, H, 2 * I, generator=g, device="cuda") * 0.02
         down = torch.randn(E, I, H, generator=g, device="cuda") * 0.02
         bias = torch.randn(E, 2 * I, generator=g, device="cuda") * 0.1
-        self.P = moe8.pack(dev, gate_up, down, gu_bias=bias)
+        self.P = moe8.pack(dev, gate_up, down, gu_bias=bias, kblock=self.kblock)
         self.host_w = (gate_up[:k].cpu(), down[:k].cpu(), bias[:k].cpu())  # (the CPU baseline's experts)
         del gate_up, down
         nsets = E // k
@@ -327,7 +330,10 @@ def main():
 
     from dense_reader import linear
 
-    wl = Workload(a.config, linear, torch)
+    if a.kblock and not CONFIGS[a.config][4].get("moe"):
+        print("bench.py: --kblock applies to the moe config only", file=sys.stderr)
+        sys.exit(2)
+    wl = Workload(a.config, linear, torch, a.kblock)
     for i in range(a.warmup):
         wl.step(i)
     torch.cuda.synchronize()
@@ -378,7 +384,8 @@ def main():
             "weight_bytes_per_call": wl.wbytes,
             "weight_copies_rotated": wl.copies,
             **({"experts": wl.moe_shape[0], "top_k": wl.moe_shape[1], "hidden": wl.moe_shape[2],
-                "intermediate": wl.moe_shape[3], "kernel": "route_gate_up (the routing and gate_up in one launch, the step's larger)"}
+                "intermediate": wl.moe_shape[3], "pack": "kblock" if wl.kblock else "bfloat4_b",
+                "kernel": "route_gate_up (the routing and gate_up in one launch, the step's larger)"}
                if wl.o.get("moe") else {}),
             "timing": "HIP graph of the timed steps, replayed; events on the replay stream",
         },

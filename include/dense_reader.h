@@ -38,6 +38,10 @@ extern "C" {
 #define DR_BFP4 1
 #define DR_BF16 2
 #define DR_INT4 3
+/* bfloat4_b with its shared exponents along K (each tile's blocks transposed: an exponent for 16 consecutive K at one
+ * N), the layout of moe8.pack(kblock=True) (moe/moe8.py:117-172, 507-527): dr_pack, dr_unpack and the expert gather of
+ * dr_moe_matmul (include/moe.h) take it; dr_matmul does not. */
+#define DR_BFP4_KB 4
 
 /* statuses */
 #define DR_OK 0

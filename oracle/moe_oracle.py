@@ -12,7 +12,9 @@ reference's root):
   [E, H, 2I] as [up | gate] columns, then y = sum_s h_s @ D_e;
 - union: the rows' distinct ids below E in increasing order (moe8.py:647-649, kernels/moe8_rows.h);
 - route: the router, one row at a time in plain Python (moe8.py:1139-1286): keys, optional group-limited routing,
-  the top k by key with the lower id first among equal keys, the softmax or sigmoid weights, the scale, a fixed slot.
+  the top k by key with the lower id first among equal keys, the softmax or sigmoid weights, the scale, a fixed slot;
+- held_kblock: the values a kblock pack holds (moe8.py:117-154 with kblock, 507-527): BFP4_b's rounding with each
+  face row 16 consecutive K at one N.
 
 What pins each function (tests/test_oracle.py, test_moe_oracle_*):
 - glu: closed forms (silu(0) = 0, the gelu_tanh constants against torch's gelu(approximate="tanh"), the clamps of
@@ -22,7 +24,10 @@ What pins each function (tests/test_oracle.py, test_moe_oracle_*):
   minus x U zeroing h -- and a hand-worked two-expert case;
 - union: brute force on small id sets (duplicates, ids past E);
 - route: brute-force sort on small rows with ties (the lower id first), the softmax weights summing to the scale,
-  a hand-built group case where the best single expert sits in a dropped group.
+  a hand-built group case where the best single expert sits in a dropped group;
+- held_kblock: against the BFP4_b tiles of the matrix with every 32 x 32 block transposed in place (the reference's
+  kblock conversion), their values turned back, bit for bit, and against a hand-made matrix whose 16-K groups each
+  hold one large value (the rest of the group rounds to its grid, the 16-N rounding would not).
 """
 
 import math
@@ -49,6 +54,16 @@ def glu(g, u, act):
         gc = np.minimum(g, OAI_LIMIT)
         return gc * _sigmoid(OAI_ALPHA * gc) * (np.clip(u, -OAI_LIMIT, OAI_LIMIT) + 1.0)
     raise ValueError(act)
+
+
+def held_kblock(w):
+    """The values a kblock BFP4_b pack holds for the float [K, N] matrix w (K, N multiples of 32): each shared
+    exponent covers 16 consecutive K at one N (reference moe8.py:117-154, the tile's block transposed before the
+    rounding), so it is dense_oracle.held of w transposed, transposed back."""
+    from oracle import dense_oracle as O
+
+    w = np.asarray(w, np.float32)
+    return np.ascontiguousarray(O.held(np.ascontiguousarray(w.T), "bfp4").T)
 
 
 def _bf16(a):

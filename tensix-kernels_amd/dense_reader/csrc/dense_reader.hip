@@ -50,7 +50,13 @@ __host__ __device__ constexpr int tile_w() {
 }
 
 __host__ __device__ constexpr int kblk(int fmt) {
-    return fmt == DR_BFP8 ? 64 : (fmt == DR_BFP4 || fmt == DR_INT4) ? 128 : 32;
+    return fmt == DR_BFP8 ? 64 : (fmt == DR_BFP4 || fmt == DR_INT4 || fmt == DR_BFP4_KB) ? 128 : 32;
+}
+
+// DR_BFP4_KB: the byte of a panel's exponents that holds column c's exponent for k (one a 16-k group): per 128-k block
+// 128 bytes, lane (kq, c) of the block's wavefront load at 2 (16 kq + c), its two groups (k 32 kq + 0..15, + 16..31)
+__host__ __device__ constexpr int exp_off_kb(int k, int c) {
+    return (k >> 7) * 128 + (((k & 127) >> 5) * 16 + c) * 2 + ((k & 31) >> 4);
 }
 
 // the byte of a panel's exponents that holds k (see the layout above)
@@ -349,6 +355,111 @@ __device__ __forceinline__ void chunk_bfp4(const Args& a, const uint8_t* const* 
         bfp4_step<0, MR, PW>(acc, xs, c[u].c);
     }
     dot_fence(acc);
+}
+
+// DR_BFP4_KB: bfp4_step with the lane's two 16-k exponent groups apart: dwords 0 and 1 (k 0..15 of the lane's 32)
+// into t0, dwords 2 and 3 into t1 (the same hazard rules; t0's last dot lies at least eight dot2c before any reader)
+template <int D, int MR, int PW>
+__device__ __forceinline__ void bfp4k_step(float (&t0)[PW][MR], float (&t1)[PW][MR], const uint32_t (&xs)[PW][MR],
+                                           const uint4 (&c)[PW]) {
+    constexpr uint32_t MAGIC = 0x43434343u;
+#pragma unroll
+    for (int q = 0; q < PW; ++q) {
+        const uint32_t w = D == 0 ? c[q].x : D == 1 ? c[q].y : D == 2 ? c[q].z : c[q].w;
+        const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+        const uint32_t a0 = __builtin_amdgcn_perm(MAGIC, lo, 0x04010400u);
+        const uint32_t a1 = __builtin_amdgcn_perm(MAGIC, lo, 0x04030402u);
+        const uint32_t a2 = __builtin_amdgcn_perm(MAGIC, hi, 0x04010400u);
+        const uint32_t a3 = __builtin_amdgcn_perm(MAGIC, hi, 0x04030402u);
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            float& acc = D < 2 ? t0[q][m] : t1[q][m];
+            dot2_bcast<4 * D + 0, D == 0>(acc, xs[q][m], a0);
+            dot2_bcast<4 * D + 1, false>(acc, xs[q][m], a1);
+            dot2_bcast<4 * D + 2, false>(acc, xs[q][m], a2);
+            if (D == 3 && q == PW - 1 && m == MR - 1)
+                dot2_bcast<4 * D + 3, false, true>(acc, xs[q][m], a3);
+            else
+                dot2_bcast<4 * D + 3, false>(acc, xs[q][m], a3);
+        }
+    }
+    if constexpr (D + 1 < 4) bfp4k_step<D + 1, MR, PW>(t0, t1, xs, c);
+}
+
+// DR_BFP4_KB, one chunk of up to two exponent groups (4 blocks of 128 k). A lane (kq, c) of a block holds 32
+// consecutive k of column c, two exponent groups of 16: its dot products over each group take x as it is (bf16 pairs,
+// broadcast across the row of 16 lanes) against the bf16 136 + m; less 136 times the group's x sum (the row's lanes
+// 0..7 or 8..15 hold its pairs), times 2^(E - 129) of the lane's group, added to the lane's sum: two FMAs a block.
+template <int MR, int PW>
+__device__ __forceinline__ void chunk_bfp4k(const Args& a, const uint8_t* const* cb, const uint8_t* const* eb, int k0,
+                                            int k1, int lane, float (&acc)[PW][MR]) {
+    const int kq = lane >> 4, i = lane & 15;
+    const int g0 = k0 >> 8;
+    const bool two = k1 - k0 > 256;
+    const int g1 = two ? g0 + 1 : g0;
+    uint32_t xp[4][MR];
+    uint32_t ex[4][PW];
+    Codes<PW> c[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int b = 2 * (u < 2 ? g0 : g1) + (u & 1);
+        const int kp = b * 128 + kq * 32 + 2 * i;
+        const int kc = min(kp, a.k - 2);
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            const int mc = min(m, a.m - 1);
+            const uint32_t v = *reinterpret_cast<const uint32_t*>(a.x + (size_t)mc * a.ldx + kc);
+            xp[u][m] = v & opaque((kp < a.k && m < a.m) ? 0xFFFFFFFFu : 0u);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int b = 2 * (u < 2 ? g0 : g1) + (u & 1);
+#pragma unroll
+        for (int q = 0; q < PW; ++q)
+            ex[u][q] = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(eb[q] + (size_t)b * 128) + lane);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int b = 2 * (u < 2 ? g0 : g1) + (u & 1);
+#pragma unroll
+        for (int q = 0; q < PW; ++q) c[u].c[q] = ld_stream16(cb[q] + (uint32_t)(b * 1024 + lane * 16));
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        if (u == 2 && !two) break;
+        uint32_t xs[PW][MR];
+        float rs0[MR], rs1[MR];  // 136 times the row's x sums over the two groups
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            const float v = bf16_to_f32(xp[u][m] & 0xFFFFu) + bf16_to_f32(xp[u][m] >> 16);
+            float v0 = i < 8 ? v : 0.f, v1 = i < 8 ? 0.f : v;
+            v0 = wsel::add_xor<8>(wsel::add_xor<4>(wsel::add_xor<2>(wsel::add_xor<1>(v0))));
+            v1 = wsel::add_xor<8>(wsel::add_xor<4>(wsel::add_xor<2>(wsel::add_xor<1>(v1))));
+            rs0[m] = 136.f * v0;
+            rs1[m] = 136.f * v1;
+#pragma unroll
+            for (int q = 0; q < PW; ++q) xs[q][m] = xp[u][m];
+        }
+        float t0[PW][MR], t1[PW][MR];
+#pragma unroll
+        for (int q = 0; q < PW; ++q)
+#pragma unroll
+            for (int m = 0; m < MR; ++m) t0[q][m] = t1[q][m] = 0.f;
+        bfp4k_step<0, MR, PW>(t0, t1, xs, c[u].c);
+        dot_fence(t0);
+        dot_fence(t1);
+#pragma unroll
+        for (int q = 0; q < PW; ++q) {
+            const float s0 = __builtin_ldexpf(1.f, (int)(ex[u][q] & 0xFFu) - 129);
+            const float s1 = __builtin_ldexpf(1.f, (int)((ex[u][q] >> 8) & 0xFFu) - 129);
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                acc[q][m] = __builtin_fmaf(t0[q][m] - rs0[m], s0, acc[q][m]);
+                acc[q][m] = __builtin_fmaf(t1[q][m] - rs1[m], s1, acc[q][m]);
+            }
+        }
+    }
 }
 
 // int4 (W4A16): the bfloat4_b code layout with no exponents (every value q = u - 8) and a bf16 scale per column and 32
@@ -943,7 +1054,7 @@ __global__ __launch_bounds__(512) void dr_gemv(const Args a) {
 // per expert further on. Down modes: the launch's K is the units' blocks of ekp rows one after another; a chunk lies in
 // one unit (ekp is a multiple of the chunk), whose expert gives that chunk's weights and whose ek values of x sit at
 // unit * ek.
-template <int MR, int PW, int MOE>
+template <int MR, int PW, int MOE, bool KB>
 __global__ __launch_bounds__(512) void dr_gemv_moe(const MoeArgs a) {
     extern __shared__ float part[];  // [W][PW][MR][16]
     __shared__ float tval[MR][TILE];
@@ -1023,6 +1134,14 @@ __global__ __launch_bounds__(512) void dr_gemv_moe(const MoeArgs a) {
         for (int q = 0; q < PW; ++q)
 #pragma unroll
             for (int m = 0; m < MR; ++m) acc[q][m] = sx[q][m] = 0.f;
+        if constexpr (KB) {  // (the lanes' sums are already scaled, their x sums taken off)
+            chunk_bfp4k<MR, PW>(b, cbx, ebx, k0, k1, lane, acc);
+#pragma unroll
+            for (int q = 0; q < PW; ++q)
+#pragma unroll
+                for (int m = 0; m < MR; ++m) wsum[q][m] += wsel::add_xor<32>(wsel::add_xor<16>(acc[q][m]));
+            return;
+        }
         chunk_bfp4<MR, PW>(b, cbx, ebx, k0, k1, lane, acc, sx);
         // the chunk's column sums less the wavefront's 136 * sum x', as dr_gemv's
 #pragma unroll
@@ -1259,6 +1378,73 @@ __device__ __forceinline__ void mgroup_bfp4(const Args& a, const uint8_t* const*
         }
 }
 
+// DR_BFP4_KB: B for the 8 values of dword D, the lane's own column at its own exponent group (no broadcast): u = m + 8
+// moved to the top of a byte with its top bit flipped is 16 m as a signed byte, times s = 2^(E - 133) of the group
+template <int D>
+__device__ __forceinline__ uint4 b_bfp4k(uint32_t w, float s) {
+    const uint32_t lo = ((w << 4) & 0xF0F0F0F0u) ^ 0x80808080u;  // k 8D + 0..3
+    const uint32_t hi = (w & 0xF0F0F0F0u) ^ 0x80808080u;         // k 8D + 4..7
+    float p[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) p[j] = (float)(int)(signed char)(lo >> (8 * j)) * s;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) p[4 + j] = (float)(int)(signed char)(hi >> (8 * j)) * s;
+    return make_uint4(pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]), pack_bf16(p[4], p[5]), pack_bf16(p[6], p[7]));
+}
+
+// DR_BFP4_KB, one exponent group of 256 k (2 blocks of 128), as mgroup_bfp4: MFMA D of block b takes k = 128 b +
+// 32 kq + 8 D + j, in the lane's group D / 2
+template <int MT, int PW>
+__device__ __forceinline__ void mgroup_bfp4k(const Args& a, const uint8_t* const* cb, const uint8_t* const* eb, int g,
+                                             int lane, f32x4 (&acc)[PW][MT]) {
+    const int r = lane & 15, kq = lane >> 4;
+    uint4 A[2][4][MT];
+    uint32_t e[2][PW];
+    uint4 c[2][PW];
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+#pragma unroll
+            for (int tt = 0; tt < MT; ++tt) A[b][d][tt] = x_row8(a, 16 * tt + r, (2 * g + b) * 128 + 32 * kq + 8 * d);
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int q = 0; q < PW; ++q)
+            e[b][q] = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(eb[q] + (size_t)(2 * g + b) * 128) + lane);
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int q = 0; q < PW; ++q)
+            c[b][q] = ld_stream16(cb[q] + (uint32_t)((2 * g + b) * 1024 + lane * 16));
+    if (a.k != a.k_pad && (g + 1) * 256 > a.k) {  // (a ragged K's last group only)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int d = 0; d < 4; ++d)
+#pragma unroll
+                for (int tt = 0; tt < MT; ++tt) x_kmask(A[b][d][tt], a, (2 * g + b) * 128 + 32 * kq + 8 * d);
+    }
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int q = 0; q < PW; ++q) {
+            const float s0 = __builtin_ldexpf(1.f, (int)(e[b][q] & 0xFFu) - 133);
+            const float s1 = __builtin_ldexpf(1.f, (int)((e[b][q] >> 8) & 0xFFu) - 133);
+            const uint4 B0 = b_bfp4k<0>(c[b][q].x, s0);
+            const uint4 B1 = b_bfp4k<1>(c[b][q].y, s0);
+            const uint4 B2 = b_bfp4k<2>(c[b][q].z, s1);
+            const uint4 B3 = b_bfp4k<3>(c[b][q].w, s1);
+#pragma unroll
+            for (int tt = 0; tt < MT; ++tt) {
+                acc[q][tt] = mfma(A[b][0][tt], B0, acc[q][tt]);
+                acc[q][tt] = mfma(A[b][1][tt], B1, acc[q][tt]);
+                acc[q][tt] = mfma(A[b][2][tt], B2, acc[q][tt]);
+                acc[q][tt] = mfma(A[b][3][tt], B3, acc[q][tt]);
+            }
+        }
+}
+
 // bf16, 4 blocks of 32 k: the lane's 8 values are its B as they are (k = 32 b + 8 kq + j)
 template <int MT, int PW>
 __device__ __forceinline__ void mgroup_bf16(const Args& a, const uint8_t* const* cb, int b0, int lane,
@@ -1335,7 +1521,7 @@ __global__ __launch_bounds__(512) void dr_mfma(const Args a) {
     if (nparts) epilogue<ROWS, PW>(a, sg, t, part, nparts, tval, tkey, wave, lane, pre);
 }
 
-template <int MT, int PW, int MOE>
+template <int MT, int PW, int MOE, bool KB>
 __global__ __launch_bounds__(512) void dr_mfma_moe(const MoeArgs a) {
     constexpr int ROWS = 16 * MT;
     extern __shared__ float part[];  // [W][PW][ROWS][16]
@@ -1380,7 +1566,12 @@ __global__ __launch_bounds__(512) void dr_mfma_moe(const MoeArgs a) {
 #pragma unroll
         for (int tt = 0; tt < MT; ++tt) acc[q][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
     auto chunk = [&](const Args& b, const uint8_t* const* cbx, const uint8_t* const* ebx, int k0, int k1) {
-        for (int gg = k0 >> 8; gg < (k1 >> 8); ++gg) mgroup_bfp4<MT, PW>(b, cbx, ebx, gg, lane, acc);
+        for (int gg = k0 >> 8; gg < (k1 >> 8); ++gg) {
+            if constexpr (KB)
+                mgroup_bfp4k<MT, PW>(b, cbx, ebx, gg, lane, acc);
+            else
+                mgroup_bfp4<MT, PW>(b, cbx, ebx, gg, lane, acc);
+        }
     };
     const int ch1 = min((split + 1) * a.cps, a.chunks);
     for (int ch = split * a.cps + wave; ch < ch1; ch += a.waves) {
@@ -1525,6 +1716,41 @@ __global__ __launch_bounds__(256) void dr_pack_k(const float* __restrict__ w, lo
     }
 }
 
+// DR_BFP4_KB: one thread a (column, 16-k group): the group's shared exponent and its 16 codes (bfloat4_b's rounding,
+// bfp_face_row, over 16 consecutive K at one N), the codes in bfloat4_b's code layout (two dwords of the lane's four)
+__global__ __launch_bounds__(256) void dr_pack_kb_k(const float* __restrict__ w, long long ld_w, int n, int k,
+                                                    const float* __restrict__ cdiv, uint8_t* __restrict__ codes,
+                                                    uint8_t* __restrict__ exps, int n_pad, int k_pad) {
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const int kgroups = k_pad / 16;
+    if (idx >= (long long)n_pad * kgroups) return;
+    const int col = (int)(idx / kgroups), kg = (int)(idx % kgroups);
+    const int p = col / 16, c = col % 16, k0 = kg * 16;
+    const float d = (cdiv != nullptr && col < n) ? cdiv[col] : 1.f;
+    float v[16];
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+        const int kk = k0 + t;
+        float x = (col < n && kk < k) ? w[(long long)col * ld_w + kk] : 0.f;
+        if (cdiv != nullptr && col < n) x = x / d;
+        v[t] = x;
+    }
+    int sm[16];
+    const uint32_t ex = bfp_face_row<3>(v, sm);
+    exps[(size_t)p * k_pad + exp_off_kb(k0, c)] = (uint8_t)ex;
+    const int b = k0 / 128, kq = (k0 % 128) / 32, h = (k0 % 32) / 16;
+    uint32_t word[2] = {0u, 0u};
+#pragma unroll
+    for (int half = 0; half < 2; ++half)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t ulo = (uint32_t)(sm[8 * half + j] + 8), uhi = (uint32_t)(sm[8 * half + 4 + j] + 8);
+            word[half] |= (ulo | (uhi << 4)) << (8 * j);
+        }
+    *reinterpret_cast<uint2*>(codes + (size_t)p * (k_pad / 128) * 1024 + (size_t)b * 1024 + (kq * 16 + c) * 16 + h * 8) =
+        make_uint2(word[0], word[1]);
+}
+
 template <int FMT>
 __global__ __launch_bounds__(256) void dr_unpack_k(const uint8_t* __restrict__ codes, const uint8_t* __restrict__ exps,
                                                    int n, int k, int k_pad, float* __restrict__ out, long long ld_out) {
@@ -1540,7 +1766,7 @@ __global__ __launch_bounds__(256) void dr_unpack_k(const uint8_t* __restrict__ c
         const uint16_t h = *reinterpret_cast<const uint16_t*>(pbase + (size_t)b * 1024 + (kq * 16 + c) * 16 + 2 * i);
         val = bf16_to_f32(h);
     } else {
-        const int e = exps[(size_t)p * k_pad + exp_off(FMT, kk)];
+        const int e = exps[(size_t)p * k_pad + (FMT == DR_BFP4_KB ? exp_off_kb(kk, c) : exp_off(FMT, kk))];
         int m;
         if (FMT == DR_BFP8) {
             const int b = kk / 64, kq = (kk % 64) / 16, i = kk % 16;
@@ -1744,17 +1970,23 @@ template <int MR, int PW, int MOE>
 void launch_gemv_moe(const MoeArgs& a, int grid, hipStream_t st) {
     const dim3 b(64 * a.waves);
     const size_t lds = (size_t)max(a.waves, a.splits) * PW * MR * 16 * sizeof(float);
-    hipLaunchKernelGGL((dr_gemv_moe<MR, PW, MOE>), dim3(grid), b, lds, st, a);
+    if (a.seg[0].fmt == DR_BFP4_KB)
+        hipLaunchKernelGGL((dr_gemv_moe<MR, PW, MOE, true>), dim3(grid), b, lds, st, a);
+    else
+        hipLaunchKernelGGL((dr_gemv_moe<MR, PW, MOE, false>), dim3(grid), b, lds, st, a);
 }
 
 template <int MT, int PW, int MOE>
 void launch_mfma_moe(const MoeArgs& a, int grid, hipStream_t st) {
     const dim3 b(64 * a.waves);
     const size_t lds = (size_t)max(a.waves, a.splits) * PW * 16 * MT * 16 * sizeof(float);
-    hipLaunchKernelGGL((dr_mfma_moe<MT, PW, MOE>), dim3(grid), b, lds, st, a);
+    if (a.seg[0].fmt == DR_BFP4_KB)
+        hipLaunchKernelGGL((dr_mfma_moe<MT, PW, MOE, true>), dim3(grid), b, lds, st, a);
+    else
+        hipLaunchKernelGGL((dr_mfma_moe<MT, PW, MOE, false>), dim3(grid), b, lds, st, a);
 }
 
-// one pass of an expert-gathered launch (bfloat4_b): the one-row modes on the GEMV; the rows modes on the GEMV up to
+// one pass of an expert-gathered launch (bfloat4_b, or its kblock packs): the one-row modes on the GEMV; the rows modes on the GEMV up to
 // two rows, else the MFMA kernel (16 rows a pass for gate/up, 16 or 32 for down)
 hipError_t launch_moe(const MoeArgs& a, int mode, int rows, int pw, int grid, hipStream_t st) {
     const bool narrow = pw == 2;  // (gate/up modes: 16-column tiles; down modes: pw 1)
@@ -1810,11 +2042,11 @@ extern "C" {
 
 int64_t dr_codes_bytes(int fmt, int k_pad, int n_pad) {
     const int64_t v = (int64_t)k_pad * n_pad;
-    return fmt == DR_BFP8 ? v : (fmt == DR_BFP4 || fmt == DR_INT4) ? v / 2 : 2 * v;
+    return fmt == DR_BFP8 ? v : (fmt == DR_BFP4 || fmt == DR_INT4 || fmt == DR_BFP4_KB) ? v / 2 : 2 * v;
 }
 
 int64_t dr_exps_bytes(int fmt, int k_pad, int n_pad) {
-    return (fmt == DR_BFP8 || fmt == DR_BFP4) ? (int64_t)k_pad * n_pad / 16 : 0;
+    return (fmt == DR_BFP8 || fmt == DR_BFP4 || fmt == DR_BFP4_KB) ? (int64_t)k_pad * n_pad / 16 : 0;
 }
 
 int64_t dr_int4_scales_bytes(int k_pad, int n_pad) { return (int64_t)(k_pad / 128) * 4 * n_pad * 2; }
@@ -1842,13 +2074,18 @@ int dr_pack_int4_scales(const uint16_t* s, int64_t ld_s, int n, int k, void* out
 int dr_pack(const float* w, int64_t ld_w, int n, int k, int fmt, const float* col_div, void* codes, void* exps,
             int n_pad, int k_pad, void* stream) {
     if (w == nullptr || codes == nullptr || n <= 0 || k <= 0 || n_pad < n || n_pad % 32 || k_pad < k ||
-        k_pad % KALIGN || ld_w < k || (fmt != DR_BF16 && exps == nullptr) || fmt < 0 || fmt > 2)
+        k_pad % KALIGN || ld_w < k || (fmt != DR_BF16 && exps == nullptr) || fmt < 0 || fmt > DR_BFP4_KB ||
+        fmt == DR_INT4)
         return DR_EINVAL;
     const long long total = (long long)(n_pad / 16) * (k_pad / 8);
     const int grid = (int)((total + 255) / 256);
     auto* c8 = reinterpret_cast<uint8_t*>(codes);
     auto* e8 = reinterpret_cast<uint8_t*>(exps);
-    if (fmt == DR_BFP8)
+    if (fmt == DR_BFP4_KB) {
+        const long long tk = (long long)n_pad * (k_pad / 16);
+        hipLaunchKernelGGL(dr_pack_kb_k, dim3((int)((tk + 255) / 256)), dim3(256), 0, S(stream), w, (long long)ld_w, n, k,
+                           col_div, c8, e8, n_pad, k_pad);
+    } else if (fmt == DR_BFP8)
         hipLaunchKernelGGL(dr_pack_k<DR_BFP8>, dim3(grid), dim3(256), 0, S(stream), w, (long long)ld_w, n, k, col_div, c8, e8, n_pad, k_pad);
     else if (fmt == DR_BFP4)
         hipLaunchKernelGGL(dr_pack_k<DR_BFP4>, dim3(grid), dim3(256), 0, S(stream), w, (long long)ld_w, n, k, col_div, c8, e8, n_pad, k_pad);
@@ -1860,7 +2097,7 @@ int dr_pack(const float* w, int64_t ld_w, int n, int k, int fmt, const float* co
 int dr_unpack(const void* codes, const void* exps, int fmt, int n, int k, int n_pad, int k_pad, float* out,
               int64_t ld_out, void* stream) {
     if (codes == nullptr || out == nullptr || n <= 0 || k <= 0 || n > n_pad || k > k_pad || k_pad % KALIGN ||
-        n_pad % 32 || ld_out < n || (fmt != DR_BF16 && exps == nullptr) || fmt < 0 || fmt > 2)
+        n_pad % 32 || ld_out < n || (fmt != DR_BF16 && exps == nullptr) || fmt < 0 || fmt > DR_BFP4_KB || fmt == DR_INT4)
         return DR_EINVAL;
     const long long total = (long long)n * k;
     const int grid = (int)((total + 255) / 256);
@@ -1870,6 +2107,8 @@ int dr_unpack(const void* codes, const void* exps, int fmt, int n, int k, int n_
         hipLaunchKernelGGL(dr_unpack_k<DR_BFP8>, dim3(grid), dim3(256), 0, S(stream), c8, e8, n, k, k_pad, out, (long long)ld_out);
     else if (fmt == DR_BFP4)
         hipLaunchKernelGGL(dr_unpack_k<DR_BFP4>, dim3(grid), dim3(256), 0, S(stream), c8, e8, n, k, k_pad, out, (long long)ld_out);
+    else if (fmt == DR_BFP4_KB)
+        hipLaunchKernelGGL(dr_unpack_k<DR_BFP4_KB>, dim3(grid), dim3(256), 0, S(stream), c8, e8, n, k, k_pad, out, (long long)ld_out);
     else
         hipLaunchKernelGGL(dr_unpack_k<DR_BF16>, dim3(grid), dim3(256), 0, S(stream), c8, e8, n, k, k_pad, out, (long long)ld_out);
     return hip_status(hipGetLastError());
@@ -1889,8 +2128,9 @@ int dr_plan(int k, int m, int32_t* chunks, int32_t* kch, int32_t* rpp) {
 
 namespace {
 
-// the launch's arguments, its panel width, tiles and rows a pass (shared by dr_matmul and dr_workspace_bytes)
-int prepare(const dr_launch* L, Args& a, int& pw, int& tiles, int& mr, bool narrow_ok = true) {
+// the launch's arguments, its panel width, tiles and rows a pass (shared by dr_matmul and dr_workspace_bytes; for the
+// expert gather, gather = true: no 16-column tiles here, and the kblock format allowed)
+int prepare(const dr_launch* L, Args& a, int& pw, int& tiles, int& mr, bool gather = false) {
     if (L == nullptr || L->x == nullptr || L->y == nullptr || L->m <= 0 || L->k <= 0 || L->k % 32 ||
         L->ldx < L->k || L->nseg < 1 || L->nseg > 4)
         return DR_EINVAL;
@@ -1913,8 +2153,8 @@ int prepare(const dr_launch* L, Args& a, int& pw, int& tiles, int& mr, bool narr
     for (int i = 0; i < L->nseg; ++i) {
         const dr_segment& s = L->seg[i];
         SegDev& d = a.seg[i];
-        const bool bfp = s.fmt == DR_BFP8 || s.fmt == DR_BFP4;
-        if (s.fmt < 0 || s.fmt > 3 || s.n <= 0 || s.n_pad < s.n || s.n_pad % 32 || s.col0 < 0 || s.col0 % 32 ||
+        const bool bfp = s.fmt == DR_BFP8 || s.fmt == DR_BFP4 || s.fmt == DR_BFP4_KB;
+        if (s.fmt < 0 || s.fmt > (gather ? DR_BFP4_KB : DR_INT4) || s.n <= 0 || s.n_pad < s.n || s.n_pad % 32 || s.col0 < 0 || s.col0 % 32 ||
             s.codes == nullptr || (bfp && s.exps == nullptr) || s.glu < 0 || s.glu > 2 || (s.glu ? 4 : 2) != pw)
             return DR_EINVAL;
         // an int4 weight alone: one segment, no GLU, residual or top-k, its group scales given
@@ -1985,7 +2225,7 @@ int prepare(const dr_launch* L, Args& a, int& pw, int& tiles, int& mr, bool narr
     // 32-column tiles than CUs, or a count just past a multiple of the CUs): each column's sums are made by the same
     // lanes in the same order whatever the tile width, so the results are the same bit for bit. (Not with top-k
     // records, one a 32-column tile, nor a GLU's pairs.)
-    if (narrow_ok && pw == 2 && mr <= 2 && a.rec == nullptr && narrow_better(tiles)) {
+    if (!gather && pw == 2 && mr <= 2 && a.rec == nullptr && narrow_better(tiles)) {
         pw = 1;
         tiles = 0;
         for (int i = 0; i < a.nseg; ++i) {
@@ -2104,7 +2344,7 @@ int prepare_moe(const dr_launch* L, const dr_moe* M, MoeArgs& a, int& pw, int& t
         M->codes_stride <= 0 || M->exps_stride <= 0)
         return DR_EINVAL;
     const dr_segment& s0 = L->seg[0];
-    if (L->nseg != 1 || L->residual != nullptr || L->topk.records != nullptr || s0.fmt != DR_BFP4 ||
+    if (L->nseg != 1 || L->residual != nullptr || L->topk.records != nullptr || (s0.fmt != DR_BFP4 && s0.fmt != DR_BFP4_KB) ||
         s0.scale != nullptr || s0.scale_up != nullptr || s0.col0 != 0 || (s0.glu == 2) != nmode || (!nmode && s0.glu))
         return DR_EINVAL;
     if (L->m < 1 || L->m > (rows ? M->id_rows : 1)) return DR_EINVAL;
@@ -2121,7 +2361,7 @@ int prepare_moe(const dr_launch* L, const dr_moe* M, MoeArgs& a, int& pw, int& t
         B.k = units * ekp;  // (the gathered K, each unit's block padded)
         B.ldx = std::max(L->ldx, B.k);
     }
-    const int st = prepare(&B, a, pw, tiles, mr, false);
+    const int st = prepare(&B, a, pw, tiles, mr, true);
     if (st != DR_OK) return st;
     a.ldx = L->ldx;
     a.ids = M->ids;

@@ -45,6 +45,7 @@ from dense_reader import pack_cache as pc  # noqa: E402
 TILE = 32
 TB = 576  # a BFP4_b tile of the reference: 64 exponent bytes, 512 bytes of sign + 3-bit magnitudes
 DR_BFP4 = 1
+DR_BFP4_KB = 4  # bfloat4_b's rounding with the shared exponent over 16 consecutive K at one N (kblock packs)
 ACTS = {"silu": 0, "gelu_tanh": 1, "swiglu_oai": 2}
 OAI_ALPHA, OAI_LIMIT = 1.702, 7.0
 
@@ -156,9 +157,10 @@ def _geometry(E, H, I):
     return sizes, (gk, gn, dk, dn)
 
 
-def _pack_one(d, w_nk, n, k, codes, exps, n_pad, k_pad):
-    """dr_pack of a float32 [N][K] device matrix into codes / exps (device uint8 views) as bfloat4_b."""
-    st = _lib.lib().dr_pack(w_nk.data_ptr(), k, n, k, DR_BFP4, None, codes.data_ptr(), exps.data_ptr(), n_pad, k_pad,
+def _pack_one(d, w_nk, n, k, codes, exps, n_pad, k_pad, fmt):
+    """dr_pack of a float32 [N][K] device matrix into codes / exps (device uint8 views) as bfloat4_b (fmt DR_BFP4) or
+    its kblock packs (DR_BFP4_KB)."""
+    st = _lib.lib().dr_pack(w_nk.data_ptr(), k, n, k, fmt, None, codes.data_ptr(), exps.data_ptr(), n_pad, k_pad,
                             d.stream())
     _lib.check(st, "dr_pack (moe8)")
 
@@ -169,9 +171,11 @@ def _bias_rows(gu_bias, I):
     return torch.stack([b[:, I:], b[:, :I]], dim=1).contiguous()
 
 
-def _pack_device(d, gate_up, down, gu_bias=None):
+def _pack_device(d, gate_up, down, gu_bias=None, kblock=False):
     """The packed arrays on the device: gu [E, 2, codes] (gate, up), gu_exps [E, 2, exps], dn [E, codes], dn_exps
-    [E, exps], bias [E, 2, I] bf16 or None. One expert at a time goes to the device in float32."""
+    [E, exps], bias [E, 2, I] bf16 or None. One expert at a time goes to the device in float32. kblock: each shared
+    exponent covers 16 consecutive K at one N (the codes keep bfloat4_b's layout; the exponents their own order)."""
+    fmt = DR_BFP4_KB if kblock else DR_BFP4
     E, H, I2 = gate_up.shape
     I = I2 // 2
     (gc, ge, dc, de), (gk, gn, dk, dn) = _geometry(E, H, I)
@@ -184,10 +188,10 @@ def _pack_device(d, gate_up, down, gu_bias=None):
         w = torch.as_tensor(gate_up[e]).to(device=t, dtype=torch.float32)  # [H, 2I] as [up | gate]
         gate = w[:, I:].t().contiguous()  # [I][H]
         up = w[:, :I].t().contiguous()
-        _pack_one(d, gate, I, H, gu[e, 0], gu_e[e, 0], gn, gk)
-        _pack_one(d, up, I, H, gu[e, 1], gu_e[e, 1], gn, gk)
+        _pack_one(d, gate, I, H, gu[e, 0], gu_e[e, 0], gn, gk, fmt)
+        _pack_one(d, up, I, H, gu[e, 1], gu_e[e, 1], gn, gk, fmt)
         dw = torch.as_tensor(down[e]).to(device=t, dtype=torch.float32).t().contiguous()  # [H][I]
-        _pack_one(d, dw, H, I, dn_c[e], dn_e[e], dn, dk)
+        _pack_one(d, dw, H, I, dn_c[e], dn_e[e], dn, dk, fmt)
     bias = _bias_rows(gu_bias, I).to(t) if gu_bias is not None else None
     return {"gu": gu, "gu_exps": gu_e, "dn": dn_c, "dn_exps": dn_e, "bias": bias}
 
@@ -234,8 +238,6 @@ def _check_weights(gate_up, down, gu_bias, kblock):
     assert E <= 1024, "moe8: at most 1024 experts"
     if gu_bias is not None:
         assert tuple(gu_bias.shape) == (E, 2 * I), (tuple(gu_bias.shape), (E, 2 * I))
-    if kblock:
-        raise NotImplementedError("moe8: kblock packs (exponents along K) are not supported by this build")
     return E, H, I
 
 
@@ -249,7 +251,7 @@ def pack_host(gate_up, down, banks, cores_per_bank=3, cache=None, gu_bias=None, 
     if cache is not None:
         arrays = pc.cache_read(cache, meta, rebuild, True, ARRAYS, "moe8", _split_hint)
     if arrays is None:
-        dv = _pack_device(dev.as_device(None), gate_up, down, gu_bias)
+        dv = _pack_device(dev.as_device(None), gate_up, down, gu_bias, kblock)
         arrays = {n: v.cpu().view(torch.int16).numpy() if v.dtype == torch.bfloat16 else v.cpu().numpy()
                   for n, v in dv.items() if v is not None}
         if cache is not None:
@@ -309,15 +311,16 @@ def pack(device, gate_up, down, cores_per_bank=3, banks=None, cache=None, gu_bia
     directory is absent or empty. A cache that differs or cannot be read raises PackCacheMismatch and is left as it
     is; rebuild=True packs again and writes over it.
 
-    gu_bias: [E, 2I] as [up | gate], added to x U and x G before the activation, held in bf16. kblock (exponents
-    along K) is not supported and raises (reference moe8.py:507-527)."""
+    gu_bias: [E, 2I] as [up | gate], added to x U and x G before the activation, held in bf16. kblock: each shared
+    exponent covers 16 consecutive K at one N instead of 16 N at one K (reference moe8.py:507-527, the tiles
+    transposed before the block-float rounding); the same ops take either pack."""
     d = dev.as_device(device)
     banks = banks or dev.dram_banks(d)
     cpb = _clamp_cpb(d, banks, cores_per_bank)
     E, H, I = _check_weights(gate_up, down, gu_bias, kblock)
     if cache is not None:
         return pack_upload(d, pack_host(gate_up, down, banks, cpb, cache, gu_bias, rebuild, kblock))
-    arrays = _pack_device(d, gate_up, down, gu_bias)
+    arrays = _pack_device(d, gate_up, down, gu_bias, kblock)
     return _device_dict(d, E, H, I, banks, cpb, arrays, bool(kblock))
 
 
@@ -494,7 +497,7 @@ def _run(P, x2, m, k_launch, ldx, y, ldy, gate_up_mode, mode, ids, ids32, w, slo
     L.act = ACTS[act]
     L.nseg = 1
     s0 = L.seg[0]
-    s0.fmt = DR_BFP4
+    s0.fmt = DR_BFP4_KB if P["kblock"] else DR_BFP4
     M = _lib.Moe()
     M.mode = mode
     M.ids, M.ld_ids = _ids_ptr(ids, ids32, id_rows, slots)

@@ -6,7 +6,8 @@ channels. Bars, relative Frobenius error and PCC above 0.9999 against the oracle
 - the conversion: the GPU pack holds bfp4_tiles' values bit for bit (the reference compares with ttnn's conversion);
 - gate_up and down (one row) below 1 % for h and y, for each activation; two loaders against one, other cores per
   bank, a split share of 0.6 and uint32 ids against the default, bit for bit; ids past E give zeros / add nothing;
-- a gate/up bias and column groups (two banks) against the oracle; column groups with one loader refused;
+- a gate/up bias and column groups (two banks) against the oracle; column groups with one loader refused; the same
+  with kblock packs (shared exponents along K), whose GPU pack holds the oracle's kblock values bit for bit;
 - gate_up_rows and down_rows (R rows, each with its own experts) below 1 %, rows past R zero; a row of the rows ops
   equals the one-row ops on that row bit for bit where one expert set is shared;
 - the same ops at the reference's default fidelity (hifi2): below 1.6 % (one arithmetic here: the same results);
@@ -17,6 +18,7 @@ channels. Bars, relative Frobenius error and PCC above 0.9999 against the oracle
 - a HIP graph of route, gate_up and down, replayed several times, equals the eager calls.
 """
 
+import ctypes
 import shutil
 import tempfile
 from pathlib import Path
@@ -25,7 +27,7 @@ import pytest
 import torch
 
 from common.testing import check, raises, same
-from dense_reader import linear
+from dense_reader import _lib, linear
 from moe import moe8
 from oracle import dense_oracle as O
 from oracle import moe_oracle as MO
@@ -39,20 +41,20 @@ REL_HIFI2 = 0.016
 FID = "hifi4"
 
 
-def on_grid(w):
-    """w's values on the BFP4_b grid (the oracle's held values), float32 [K, N]."""
-    return torch.from_numpy(O.held(w, "bfp4")).float()
+def on_grid(w, kblock=False):
+    """w's values on the BFP4_b grid (the oracle's held values; kblock: the grid of 16 consecutive K), float32 [K, N]."""
+    return torch.from_numpy(MO.held_kblock(w.numpy()) if kblock else O.held(w, "bfp4")).float()
 
 
 _EXPERTS = {}
 
 
-def experts(seed, gu_scale=0.02):
-    key = (seed, gu_scale)
+def experts(seed, gu_scale=0.02, kblock=False):
+    key = (seed, gu_scale, kblock)
     if key not in _EXPERTS:
         g = torch.Generator().manual_seed(seed)
-        gu = torch.stack([on_grid(torch.randn(H, 2 * I, generator=g) * gu_scale).to(BF) for _ in range(E)])
-        dn = torch.stack([on_grid(torch.randn(I, H, generator=g) * 0.02).to(BF) for _ in range(E)])
+        gu = torch.stack([on_grid(torch.randn(H, 2 * I, generator=g) * gu_scale, kblock).to(BF) for _ in range(E)])
+        dn = torch.stack([on_grid(torch.randn(I, H, generator=g) * 0.02, kblock).to(BF) for _ in range(E)])
         _EXPERTS[key] = (gu, dn)
     return _EXPERTS[key]
 
@@ -208,8 +210,91 @@ def test_bias_groups(device):
         check(f"{act} with a bias and column groups, {FID}: h", host(th, K * I)[:1], rh, rel=REL)
         check(f"{act} with a bias and column groups, {FID}: y", host(ty, H)[:1], ry, rel=REL)
     raises("column groups with one loader", AssertionError, lambda: moe8.gate_up(tx, P, tid, twt, K, loaders=1))
-    raises("a kblock pack", NotImplementedError, lambda: moe8.pack(device, gu, dn, kblock=True))
     rows_case(device, gu, dn, P, 6, act="swiglu_oai", gb=gb, loaders=(1, 2), seed=6)
+
+
+def test_kblock_pack(device):
+    """The GPU kblock pack (dr_pack, DR_BFP4_KB) read back by dr_unpack holds the oracle's kblock values bit for bit:
+    zeros, a tiny value, a group with one large value, and a K past the last full 256 (padded with zeros)."""
+    lib = _lib.lib()
+    for k, n in ((256, 512), (1120, 96)):
+        g = torch.Generator().manual_seed(k)
+        w = torch.randn(k, n, generator=g) * 0.02
+        w[3, 5], w[7, 9] = 0.0, -1e-30
+        w[40:56, 17] *= 300
+        k_pad, n_pad = -(-k // linear.KALIGN) * linear.KALIGN, -(-n // 32) * 32
+        fmt = moe8.DR_BFP4_KB
+        codes = torch.zeros(lib.dr_codes_bytes(fmt, k_pad, n_pad), dtype=torch.uint8, device=device.torch)
+        exps = torch.zeros(lib.dr_exps_bytes(fmt, k_pad, n_pad), dtype=torch.uint8, device=device.torch)
+        wd = w.t().contiguous().to(device.torch)
+        out = torch.full((k, n_pad), float("nan"), device=device.torch)
+        _lib.check(lib.dr_pack(wd.data_ptr(), k, n, k, fmt, None, codes.data_ptr(), exps.data_ptr(), n_pad, k_pad,
+                               device.stream()), "dr_pack")
+        _lib.check(lib.dr_unpack(codes.data_ptr(), exps.data_ptr(), fmt, n, k, n_pad, k_pad, out.data_ptr(), n_pad,
+                                 device.stream()), "dr_unpack")
+        same(f"kblock pack {k} x {n}", out[:, :n].cpu(), torch.from_numpy(MO.held_kblock(w.numpy())))
+    raises("dr_matmul refuses a kblock weight", Exception, lambda: _kblock_matmul(device))
+
+
+def _kblock_matmul(device):
+    """a dense launch of a kblock segment: dr_matmul takes only the four dense formats (DR_EINVAL raises)."""
+    L = _lib.Launch()
+    x = torch.zeros(1, 256, dtype=BF, device=device.torch)
+    y = torch.zeros(1, 32, dtype=BF, device=device.torch)
+    codes = torch.zeros(4096, dtype=torch.uint8, device=device.torch)
+    L.x, L.m, L.k, L.ldx, L.y, L.ldy, L.nseg = x.data_ptr(), 1, 256, 256, y.data_ptr(), 32, 1
+    s0 = L.seg[0]
+    s0.fmt, s0.n, s0.n_pad, s0.codes, s0.exps = moe8.DR_BFP4_KB, 32, 32, codes.data_ptr(), codes.data_ptr()
+    L.stream = torch.cuda.current_stream(device.torch).cuda_stream
+    _lib.check(_lib.lib().dr_matmul(ctypes.byref(L)), "dr_matmul")
+
+
+def test_bias_groups_kblock(device):
+    """The reference's kblock case (each shared exponent over 16 consecutive K at one N): a bias and column groups,
+    one row for each activation, the rows ops at 6 rows (the MFMA kernels) and 2 rows (the GEMV's two-row pass), and
+    the router inside gate/up equal to route then gate_up, all on the kblock pack against the oracle."""
+    gu, dn = experts(3, 0.1, kblock=True)
+    g = torch.Generator().manual_seed(4)
+    gb = torch.randn(E, 2 * I, generator=g) * 0.5
+    P = moe8.pack(device, gu, dn, banks=2, gu_bias=gb, kblock=True)
+    assert P["kblock"] and moe8.gu_groups(I // 32, 2)[0] == 2
+    for act in ("swiglu_oai", "silu"):
+        ids, wts, x, tid, twt, tx = decode_inputs(device, 5)
+        ry, rh = oracle(x, gu, dn, ids, wts, act, gb)
+        th = moe8.gate_up(tx, P, tid, twt, K, act=act, loaders=2, fidelity=FID)
+        ty = moe8.down(th, P, tid, K, loaders=2, fidelity=FID)
+        check(f"{act} with a bias, column groups and K blocks, {FID}: h", host(th, K * I)[:1], rh, rel=REL)
+        check(f"{act} with a bias, column groups and K blocks, {FID}: y", host(ty, H)[:1], ry, rel=REL)
+    raises("column groups with one loader", AssertionError, lambda: moe8.gate_up(tx, P, tid, twt, K, loaders=1))
+    rows_case(device, gu, dn, P, 6, act="swiglu_oai", gb=gb, loaders=(1, 2), seed=6)
+    rows_case(device, gu, dn, P, 2, act="silu", gb=gb, seed=7)
+    rows_case(device, gu, dn, P, 20, act="silu", gb=gb, seed=8)
+    # the router inside gate/up on a kblock pack (32 experts: the router takes E a multiple of 32): ids, weights, h
+    # and down's y the same as route then gate_up
+    Er, Hr, Ir = 32, 256, 64
+    g = torch.Generator().manual_seed(9)
+    gur = torch.stack([on_grid(torch.randn(Hr, 2 * Ir, generator=g) * 0.05, True).to(BF) for _ in range(Er)])
+    dnr = torch.stack([on_grid(torch.randn(Ir, Hr, generator=g) * 0.02, True).to(BF) for _ in range(Er)])
+    Pr = moe8.pack(device, gur, dnr, kblock=True)
+    lg = (torch.randn(1, 1, 1, Er, generator=g) * 2).to(device.torch)
+    xr = torch.randn(1, 1, 1, Hr, generator=g).to(BF).to(device.torch)
+    outs = []
+    for fused in (False, True):
+        ids = torch.full((1, 1, 1, K), 1234, dtype=torch.int16, device=device.torch)
+        w = torch.full((1, 1, 1, K), float("nan"), dtype=BF, device=device.torch)
+        if fused:
+            h = moe8.route_gate_up(lg, xr, Pr, ids, w, K, act="silu", loaders=2)
+        else:
+            moe8.route(lg, ids, w, K)
+            h = moe8.gate_up(xr, Pr, ids, w, K, act="silu", loaders=2)
+        y = moe8.down(h, Pr, ids, K)
+        outs.append([t.cpu() for t in (ids, w.view(torch.int16), h, y)])
+    for name, a, b in zip(("ids", "weights", "h", "y"), outs[1], outs[0]):
+        same(f"kblock, the router inside gate/up: {name}", a, b)
+    ids0 = outs[0][0].reshape(-1).long()
+    ry, rh = oracle(xr.cpu().reshape(1, Hr), gur, dnr, ids0, outs[0][1].view(BF).reshape(-1), "silu")
+    check("kblock, routed h against the oracle", host(outs[0][2], K * Ir)[:1], rh, rel=REL)
+    check("kblock, routed y against the oracle", host(outs[0][3], Hr)[:1], ry, rel=REL)
 
 
 def test_rows(device):

@@ -68,6 +68,22 @@ def test_bfp4_tiles_kblock_is_the_transposed_blocks():
     vals = moe8.bfp4_values(moe8.bfp4_tiles(w, kblock=True), kblock=True)
     held_t = O.held(wt, "bfp4").reshape(k // 32, 32, n // 32, 32).transpose(0, 2, 3, 1)  # blocks turned back
     assert np.array_equal(vals, held_t)
+    # the oracle's kblock values: the same tiles' values in [K, N] order
+    assert np.array_equal(MO.held_kblock(w), vals.transpose(0, 2, 1, 3).reshape(k, n))
+
+
+def test_held_kblock_groups_run_along_k():
+    """A hand-made matrix: each 16-K group at one N holds one value 1.0 and fifteen 2^-3 + 2^-5; along K those round to
+    the group's grid of 2^-2 steps (3-bit magnitudes under the exponent of 1.0): 0.15625 is 0.625 of a step, so 0.25;
+    along N (the plain pack) their face rows hold no 1.0 and keep 2^-3 + 2^-5 (magnitude 101b) exactly."""
+    w = np.full((64, 32), 2.0**-3 + 2.0**-5, np.float32)
+    w[0::16, :] = 1.0
+    h = MO.held_kblock(w)
+    assert np.all(h[0::16] == 1.0)
+    rest = np.ones(64, bool)
+    rest[0::16] = False
+    assert np.all(h[rest] == 0.25), np.unique(h[rest])
+    assert np.all(O.held(w, "bfp4")[rest] == w[rest])
 
 
 def test_moe_oracle_glu_closed_forms():

@@ -249,6 +249,41 @@ def _kblock_matmul(device):
     _lib.check(_lib.lib().dr_matmul(ctypes.byref(L)), "dr_matmul")
 
 
+def test_kblock_ragged_k(device):
+    """kblock packs where K is not a multiple of 256 (H = 2880 for gate/up, I = 1440 for down: the last exponent
+    groups half padding): one row on the GEMV and 3 rows on the MFMA kernels against the oracle, silu and
+    swiglu_oai."""
+    Eg, Hg, Ig, kg = 8, 2880, 1440, 3
+    g = torch.Generator().manual_seed(51)
+    gu = torch.stack([on_grid(torch.randn(Hg, 2 * Ig, generator=g) * 0.05, True).to(BF) for _ in range(Eg)])
+    dn = torch.stack([on_grid(torch.randn(Ig, Hg, generator=g) * 0.02, True).to(BF) for _ in range(Eg)])
+    P = moe8.pack(device, gu, dn, kblock=True)
+    R = 3
+    ids = torch.stack([torch.randperm(Eg, generator=g)[:kg] for _ in range(R)])
+    wts = torch.softmax(torch.randn(R, kg, generator=g), -1).to(BF)
+    x = torch.randn(R, Hg, generator=g).to(BF)
+    tid = ids.to(torch.int16).reshape(1, 1, R, kg).to(device.torch)
+    twt = wts.reshape(1, 1, R, kg).to(device.torch)
+    tx = x.reshape(1, 1, R, Hg).to(device.torch)
+    for act in ("silu", "swiglu_oai"):
+        refs = [oracle(x[r : r + 1], gu, dn, ids[r], wts[r], act) for r in range(R)]
+        th = moe8.gate_up(tx[:, :, :1].contiguous(), P, tid, twt, kg, act=act, loaders=2)
+        ty = moe8.down(th, P, tid, kg)
+        check(f"kblock, K past 256-multiples, {act}, one row: h", host(th, kg * Ig)[:1], refs[0][1], rel=REL)
+        check(f"kblock, K past 256-multiples, {act}, one row: y", host(ty, Hg)[:1], refs[0][0], rel=REL)
+        u = MO.union(ids.numpy(), Eg)
+        th = moe8.gate_up_rows(tx, P, tid, twt, kg, R, act=act)
+        ty = moe8.down_rows(th, P, tid, kg, R)
+        href = torch.zeros(R, len(u) * Ig, dtype=torch.float64)
+        for r in range(R):
+            for s_, e in enumerate(ids[r].tolist()):
+                q = u.index(e)
+                href[r, q * Ig : (q + 1) * Ig] = refs[r][1][0, s_ * Ig : (s_ + 1) * Ig]
+        check(f"kblock, K past 256-multiples, {act}, {R} rows: h", host(th, len(u) * Ig)[:R], href, rel=REL)
+        check(f"kblock, K past 256-multiples, {act}, {R} rows: y", host(ty, Hg)[:R],
+              torch.cat([refs[r][0] for r in range(R)]), rel=REL)
+
+
 def test_bias_groups_kblock(device):
     """The reference's kblock case (each shared exponent over 16 consecutive K at one N): a bias and column groups,
     one row for each activation, the rows ops at 6 rows (the MFMA kernels) and 2 rows (the GEMV's two-row pass), and

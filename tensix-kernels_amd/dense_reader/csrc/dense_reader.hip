@@ -433,11 +433,11 @@ __device__ __forceinline__ void chunk_bfp4k(const Args& a, const uint8_t* const*
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
             const float v = bf16_to_f32(xp[u][m] & 0xFFFFu) + bf16_to_f32(xp[u][m] >> 16);
-            float v0 = i < 8 ? v : 0.f, v1 = i < 8 ? 0.f : v;
-            v0 = wsel::add_xor<8>(wsel::add_xor<4>(wsel::add_xor<2>(wsel::add_xor<1>(v0))));
-            v1 = wsel::add_xor<8>(wsel::add_xor<4>(wsel::add_xor<2>(wsel::add_xor<1>(v1))));
-            rs0[m] = 136.f * v0;
-            rs1[m] = 136.f * v1;
+            // the sum over this lane's half of the row (lanes 0..7: group 0, 8..15: group 1), then the other half's
+            const float mine = wsel::add_xor<4>(wsel::add_xor<2>(wsel::add_xor<1>(v)));
+            const float other = __uint_as_float(wsel::dpp_xor<8>(__float_as_uint(mine)));
+            rs0[m] = 136.f * (i < 8 ? mine : other);
+            rs1[m] = 136.f * (i < 8 ? other : mine);
 #pragma unroll
             for (int q = 0; q < PW; ++q) xs[q][m] = xp[u][m];
         }

@@ -32,6 +32,22 @@ def test_library_exports_every_declared_symbol():
         assert re.search(rf"\bT {s}\b", out), s
 
 
+def test_constants_match_the_headers():
+    """The numbers the Python bindings pass (status codes, MoE modes and activations, the expert packs' formats) are
+    the ones include/*.h defines."""
+    from moe import moe8
+
+    text = "".join(h.read_text() for h in HEADERS)
+    defs = {k: int(v) for k, v in re.findall(r"^#define\s+(DR_\w+)\s+(\d+)\b", text, re.M)}
+    want = {"DR_OK": _lib.DR_OK, "DR_EINVAL": _lib.DR_EINVAL, "DR_EHIP": _lib.DR_EHIP, "DR_ERANGE": _lib.DR_ERANGE,
+            "DR_MOE_GATE_UP": _lib.DR_MOE_GATE_UP, "DR_MOE_DOWN": _lib.DR_MOE_DOWN,
+            "DR_MOE_GATE_UP_ROWS": _lib.DR_MOE_GATE_UP_ROWS, "DR_MOE_DOWN_ROWS": _lib.DR_MOE_DOWN_ROWS,
+            "DR_BFP4": moe8.DR_BFP4, "DR_BFP4_KB": moe8.DR_BFP4_KB, "DR_ACT_SILU": moe8.ACTS["silu"],
+            "DR_ACT_GELU_TANH": moe8.ACTS["gelu_tanh"], "DR_ACT_SWIGLU_OAI": moe8.ACTS["swiglu_oai"]}
+    for name, v in want.items():
+        assert defs.get(name) == v, (name, defs.get(name), v)
+
+
 def test_struct_layout_matches_c(tmp_path):
     src = tmp_path / "layout.c"
     src.write_text(

@@ -297,6 +297,11 @@ __device__ __forceinline__ void bfp4_step(float (&acc)[PW][MR], const uint32_t (
     if constexpr (D + 1 < 4) bfp4_step<D + 1, MR, PW>(acc, xs, c);
 }
 
+// the 128-K block whose codes a bfloat4_b decoder loads for block b: b itself, or where b lies wholly in the padding
+// past K, the block before it (K pads to a whole 256-K exponent group, so only an odd block can lie past K). x is
+// zero past K, so those codes add nothing; loading the other block's bytes, already in flight, reads no padding.
+__device__ __forceinline__ int real_block(int b, int k) { return b * 128 >= k ? b - 1 : b; }
+
 // bfp4: lane (kq, c) accumulates column c over k = 128 b + 32 kq + j (j < 32); lane (kq, i) makes the bf16 pair x'
 // for k = 128 b + 32 kq + 2i, +1. Weight values enter as bf16 136 + m (0x4300 | u), so acc = sum x' (136 + m) and
 // sx (per lane, the x' it made) gives the 136 * sum x' to take off. One chunk of one or two exponent groups (two
@@ -330,7 +335,7 @@ __device__ __forceinline__ void chunk_bfp4(const Args& a, const uint8_t* const* 
             e[h][q] = ld_stream4(eb[q] + (uint32_t)((h ? g1 : g0) * 256 + 4 * lane));
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-        const int b = 2 * (u < 2 ? g0 : g1) + (u & 1);
+        const int b = real_block(2 * (u < 2 ? g0 : g1) + (u & 1), a.k);
 #pragma unroll
         for (int q = 0; q < PW; ++q) c[u].c[q] = ld_stream16(cb[q] + (uint32_t)(b * 1024 + lane * 16));
     }
@@ -414,14 +419,14 @@ __device__ __forceinline__ void chunk_bfp4k(const Args& a, const uint8_t* const*
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-        const int b = 2 * (u < 2 ? g0 : g1) + (u & 1);
+        const int b = real_block(2 * (u < 2 ? g0 : g1) + (u & 1), a.k);
 #pragma unroll
         for (int q = 0; q < PW; ++q)
             ex[u][q] = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(eb[q] + (size_t)b * 128) + lane);
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-        const int b = 2 * (u < 2 ? g0 : g1) + (u & 1);
+        const int b = real_block(2 * (u < 2 ? g0 : g1) + (u & 1), a.k);
 #pragma unroll
         for (int q = 0; q < PW; ++q) c[u].c[q] = ld_stream16(cb[q] + (uint32_t)(b * 1024 + lane * 16));
     }
@@ -1347,7 +1352,7 @@ __device__ __forceinline__ void mgroup_bfp4(const Args& a, const uint8_t* const*
     for (int b = 0; b < 2; ++b)
 #pragma unroll
         for (int q = 0; q < PW; ++q)
-            c[b][q] = ld_stream16(cb[q] + (uint32_t)((2 * g + b) * 1024 + lane * 16));
+            c[b][q] = ld_stream16(cb[q] + (uint32_t)(real_block(2 * g + b, a.k) * 1024 + lane * 16));
     if (a.k != a.k_pad && (g + 1) * 256 > a.k) {  // (a ragged K's last group only)
 #pragma unroll
         for (int b = 0; b < 2; ++b)
@@ -1411,12 +1416,13 @@ __device__ __forceinline__ void mgroup_bfp4k(const Args& a, const uint8_t* const
     for (int b = 0; b < 2; ++b)
 #pragma unroll
         for (int q = 0; q < PW; ++q)
-            e[b][q] = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(eb[q] + (size_t)(2 * g + b) * 128) + lane);
+            e[b][q] = __builtin_nontemporal_load(
+                reinterpret_cast<const uint16_t*>(eb[q] + (size_t)real_block(2 * g + b, a.k) * 128) + lane);
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
         for (int q = 0; q < PW; ++q)
-            c[b][q] = ld_stream16(cb[q] + (uint32_t)((2 * g + b) * 1024 + lane * 16));
+            c[b][q] = ld_stream16(cb[q] + (uint32_t)(real_block(2 * g + b, a.k) * 1024 + lane * 16));
     if (a.k != a.k_pad && (g + 1) * 256 > a.k) {  // (a ragged K's last group only)
 #pragma unroll
         for (int b = 0; b < 2; ++b)

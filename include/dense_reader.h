@@ -158,6 +158,24 @@ int dr_topk_merge(const void* records, int n_records, int rows, int k, int fp32,
  * takes. For inspection; results depend only on what this returns. */
 int dr_plan(int k, int m, int32_t* chunks, int32_t* kch, int32_t* rows_per_pass);
 
+/* What dr_matmul would launch for this launch, for inspection (replaces the plan dict that dense_reader/linear.py:
+ * 455-495 choose/plan return): the kernel, the output tile width, the work split and the top-k records it writes. */
+typedef struct dr_launch_info {
+    int32_t kernel;        /* 0: the VALU GEMV (rows <= 2 a pass, and int4), 1: the MFMA kernel */
+    int32_t rows_per_pass;
+    int32_t tile_cols;     /* output columns of a work tile: 16 (one panel) or 32 */
+    int32_t tiles;         /* work tiles of the launch */
+    int32_t chunks;        /* K chunks a tile, kch values each */
+    int32_t kch;
+    int32_t splits;        /* workgroups a tile (split K), 1 if unsplit */
+    int32_t workgroups;    /* workgroups of one pass */
+    int32_t passes;        /* launches (row passes) */
+    int32_t records;       /* top-k records the launch writes (0: no top-k) */
+    int32_t tiles_per_record;
+    int32_t reserved[5];
+} dr_launch_info;
+int dr_launch_plan(const dr_launch* launch, dr_launch_info* info);
+
 const char* dr_status_string(int status);
 int dr_version(void);
 

@@ -28,6 +28,7 @@ SYMBOLS = (
     "dr_topk_merge",
     "dr_topk_merge_workspace_bytes",
     "dr_plan",
+    "dr_launch_plan",
     "dr_status_string",
     "dr_version",
     "dr_head_pick",
@@ -93,6 +94,23 @@ class Launch(ctypes.Structure):
         ("workspace", c_void_p),
         ("workspace_bytes", c_int64),
         ("stream", c_void_p),
+    ]
+
+
+class LaunchInfo(ctypes.Structure):
+    _fields_ = [
+        ("kernel", c_int32),
+        ("rows_per_pass", c_int32),
+        ("tile_cols", c_int32),
+        ("tiles", c_int32),
+        ("chunks", c_int32),
+        ("kch", c_int32),
+        ("splits", c_int32),
+        ("workgroups", c_int32),
+        ("passes", c_int32),
+        ("records", c_int32),
+        ("tiles_per_record", c_int32),
+        ("reserved", c_int32 * 5),
     ]
 
 
@@ -179,6 +197,8 @@ def lib():
         L.dr_topk_merge_workspace_bytes.argtypes = [c_int, c_int, c_int]
         L.dr_plan.restype = c_int
         L.dr_plan.argtypes = [c_int, c_int, ctypes.POINTER(c_int32), ctypes.POINTER(c_int32), ctypes.POINTER(c_int32)]
+        L.dr_launch_plan.restype = c_int
+        L.dr_launch_plan.argtypes = [ctypes.POINTER(Launch), ctypes.POINTER(LaunchInfo)]
         L.dr_status_string.restype = ctypes.c_char_p
         L.dr_status_string.argtypes = [c_int]
         L.dr_version.restype = c_int
@@ -209,6 +229,15 @@ def check(status, what):
     if status in (DR_EINVAL, DR_ERANGE):
         raise ValueError(msg)
     raise RuntimeError(msg)
+
+
+def launch_info(L):
+    """dr_launch_plan of a filled dr_launch: what dr_matmul would launch, as a dict ("kernel": "gemv" or "mfma")."""
+    info = LaunchInfo()
+    check(lib().dr_launch_plan(L, info), "dr_launch_plan")
+    out = {f: getattr(info, f) for f, _ in LaunchInfo._fields_ if f != "reserved"}
+    out["kernel"] = ("gemv", "mfma")[info.kernel]
+    return out
 
 
 def plan(k, m):

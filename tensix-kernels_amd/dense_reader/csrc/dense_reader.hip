@@ -270,14 +270,19 @@ __device__ __forceinline__ void chunk_bfp8(const Args& a, const uint8_t* const* 
     }
 }
 
-template <int D, int MR, int PW>
+// The nibble u = m + 8 enters a dot2c as the bf16 whose high byte is HI and low byte u: HI = 0x43 gives 128 + u = 136 + m
+// (x as it is: int4), HI = 0x3F gives (128 + u) / 256 (the folded x' of bfloat4_b, which can be as large as the
+// format allows: its products and their excess over x' m stay 2^8 further from fp32's overflow).
+constexpr uint32_t BF16_136 = 0x43434343u;
+constexpr uint32_t BF16_136_256 = 0x3F3F3F3Fu;
+
+template <int D, int MR, int PW, uint32_t MAGIC = BF16_136>
 __device__ __forceinline__ void bfp4_step(float (&acc)[PW][MR], const uint32_t (&xs)[PW][MR], const uint4 (&c)[PW]) {
-    constexpr uint32_t MAGIC = 0x43434343u;
 #pragma unroll
     for (int q = 0; q < PW; ++q) {
         const uint32_t w = D == 0 ? c[q].x : D == 1 ? c[q].y : D == 2 ? c[q].z : c[q].w;
         const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
-        // bf16 pairs 0x43uu: 128 + u = 136 + m, for k 8D + (0,1), (2,3) (low nibbles) and (4,5), (6,7) (high)
+        // bf16 pairs MAGIC-byte:u, for k 8D + (0,1), (2,3) (low nibbles) and (4,5), (6,7) (high)
         const uint32_t a0 = __builtin_amdgcn_perm(MAGIC, lo, 0x04010400u);
         const uint32_t a1 = __builtin_amdgcn_perm(MAGIC, lo, 0x04030402u);
         const uint32_t a2 = __builtin_amdgcn_perm(MAGIC, hi, 0x04010400u);
@@ -294,7 +299,7 @@ __device__ __forceinline__ void bfp4_step(float (&acc)[PW][MR], const uint32_t (
                 dot2_bcast<4 * D + 3, false>(acc[q][m], xs[q][m], a3);
         }
     }
-    if constexpr (D + 1 < 4) bfp4_step<D + 1, MR, PW>(acc, xs, c);
+    if constexpr (D + 1 < 4) bfp4_step<D + 1, MR, PW, MAGIC>(acc, xs, c);
 }
 
 // the 128-K block whose codes a bfloat4_b decoder loads for block b: b itself, or where b lies wholly in the padding
@@ -303,9 +308,10 @@ __device__ __forceinline__ void bfp4_step(float (&acc)[PW][MR], const uint32_t (
 __device__ __forceinline__ int real_block(int b, int k) { return b * 128 >= k ? b - 1 : b; }
 
 // bfp4: lane (kq, c) accumulates column c over k = 128 b + 32 kq + j (j < 32); lane (kq, i) makes the bf16 pair x'
-// for k = 128 b + 32 kq + 2i, +1. Weight values enter as bf16 136 + m (0x4300 | u), so acc = sum x' (136 + m) and
-// sx (per lane, the x' it made) gives the 136 * sum x' to take off. One chunk of one or two exponent groups (two
-// blocks each), loaded as chunk_bfp8 loads its chunk.
+// for k = 128 b + 32 kq + 2i, +1. Weight values enter as the bf16 (136 + m) / 256 (0x3F00 | u), so acc = sum x' (136 +
+// m) / 256 and sx (per lane, the x' it made) gives the (136 / 256) sum x' to take off; the caller scales the chunk's
+// difference by 256 (exact: the same value, rounded alike, as with the weights 136 + m, until those would overflow).
+// One chunk of one or two exponent groups (two blocks each), loaded as chunk_bfp8 loads its chunk.
 template <int MR, int PW>
 __device__ __forceinline__ void chunk_bfp4(const Args& a, const uint8_t* const* cb, const uint8_t* const* eb, int k0,
                                            int k1, int lane, float (&acc)[PW][MR], float (&sx)[PW][MR]) {
@@ -357,10 +363,13 @@ __device__ __forceinline__ void chunk_bfp4(const Args& a, const uint8_t* const* 
                 sx[q][m] += bf16_to_f32(p & 0xFFFFu) + bf16_to_f32(p >> 16);
             }
         }
-        bfp4_step<0, MR, PW>(acc, xs, c[u].c);
+        bfp4_step<0, MR, PW, BF16_136_256>(acc, xs, c[u].c);
     }
     dot_fence(acc);
 }
+
+// a bfloat4_b chunk's column sum (the wavefront's lanes reduced) less the excess: (acc - (136 / 256) sum x') * 256
+__device__ __forceinline__ float bfp4_chunk_sum(float acc, float sx) { return (acc - 0.53125f * sx) * 256.f; }
 
 // DR_BFP4_KB: bfp4_step with the lane's two 16-k exponent groups apart: dwords 0 and 1 (k 0..15 of the lane's 32)
 // into t0, dwords 2 and 3 into t1 (the same hazard rules; t0's last dot lies at least eight dot2c before any reader)
@@ -1016,14 +1025,13 @@ __global__ __launch_bounds__(512) void dr_gemv(const Args a) {
 #pragma unroll
                 for (int m = 0; m < MR; ++m) sx[q][m] = 0.f;
             chunk_bfp4<MR, PW>(a, cb, eb, k0, k1, lane, acc, sx);
-            // the wavefront's 136 * sum x' (every lane made distinct x'), taken off every column
+            // the wavefront's sum of x' (every lane made distinct x'): its excess is taken off every column
 #pragma unroll
             for (int q = 0; q < PW; ++q)
 #pragma unroll
                 for (int m = 0; m < MR; ++m) {
                     float v = wsel::add_xor<8>(wsel::add_xor<4>(wsel::add_xor<2>(wsel::add_xor<1>(sx[q][m]))));
-                    v = wsel::add_xor<32>(wsel::add_xor<16>(v));
-                    corr[q][m] = 136.f * v;
+                    corr[q][m] = wsel::add_xor<32>(wsel::add_xor<16>(v));
                 }
         } else {
             chunk_bf16<MR, PW>(a, cb, k0, k1, lane, acc);
@@ -1035,7 +1043,7 @@ __global__ __launch_bounds__(512) void dr_gemv(const Args a) {
             for (int m = 0; m < MR; ++m) {
                 float v = acc[q][m];
                 v = wsel::add_xor<32>(wsel::add_xor<16>(v));
-                wsum[q][m] += v - corr[q][m];
+                wsum[q][m] += fmt == DR_BFP4 ? bfp4_chunk_sum(v, corr[q][m]) : v;
             }
     }
     if (lane < 16) {
@@ -1148,7 +1156,7 @@ __global__ __launch_bounds__(512) void dr_gemv_moe(const MoeArgs a) {
             return;
         }
         chunk_bfp4<MR, PW>(b, cbx, ebx, k0, k1, lane, acc, sx);
-        // the chunk's column sums less the wavefront's 136 * sum x', as dr_gemv's
+        // the chunk's column sums less the wavefront's excess, as dr_gemv's
 #pragma unroll
         for (int q = 0; q < PW; ++q)
 #pragma unroll
@@ -1157,7 +1165,7 @@ __global__ __launch_bounds__(512) void dr_gemv_moe(const MoeArgs a) {
                 c = wsel::add_xor<32>(wsel::add_xor<16>(c));
                 float v = acc[q][m];
                 v = wsel::add_xor<32>(wsel::add_xor<16>(v));
-                wsum[q][m] += v - 136.f * c;
+                wsum[q][m] += bfp4_chunk_sum(v, c);
             }
     };
     const int ch1 = min((split + 1) * a.cps, a.chunks);
@@ -2296,6 +2304,31 @@ int dr_matmul(const dr_launch* L) {
         const hipError_t e = launch_rows(p, mr, pw, tiles * a.splits, st);
         if (e != hipSuccess) return DR_EHIP;
     }
+    return DR_OK;
+}
+
+int dr_launch_plan(const dr_launch* L, dr_launch_info* info) {
+    Args a{};
+    int pw, tiles, mr;
+    if (info == nullptr) return DR_EINVAL;
+    if (L != nullptr && L->act == DR_ACT_SWIGLU_OAI) return DR_EINVAL;
+    const int st = prepare(L, a, pw, tiles, mr);
+    if (st != DR_OK) return st;
+    *info = dr_launch_info{};
+    info->kernel = (mr >= 16) ? 1 : 0;
+    info->rows_per_pass = mr;
+    info->tile_cols = pw == 1 ? 16 : TILE;
+    info->tiles = tiles;
+    info->chunks = a.chunks;
+    info->kch = a.kch;
+    info->splits = a.splits;
+    info->workgroups = tiles * a.splits;
+    int passes = 0;
+    for (int r0 = 0; r0 < L->m; r0 += mr)
+        if (!(a.rec != nullptr && r0 >= a.tk_rows && !a.write_y)) ++passes;
+    info->passes = passes;
+    info->records = a.rec != nullptr ? tiles : 0;
+    info->tiles_per_record = a.rec != nullptr ? 1 : 0;
     return DR_OK;
 }
 

@@ -383,6 +383,37 @@ def matmul(
     A block list in place of w: matmul(x, [(w_or_(gate, up), col0_tiles[, scale]), ...], None, out=None, **opts) is
     one launch, one output, over two to four column blocks of one K; each block's columns go to its col0_tiles. The
     output equals one call per block (out=, col0=) bit for bit. Block output spans must not overlap."""
+    L, y, keep = _launch(x, w, scale, topk=topk, out=out, col0=col0, w_up=w_up, max_banks=max_banks, **opts)
+    d = x.device
+    st = torch.cuda.current_stream(d)
+    L.stream = st.cuda_stream
+    need = _lib.lib().dr_workspace_bytes(L)
+    _lib.check(_lib.DR_EINVAL if need < 0 else _lib.DR_OK, "dr_workspace_bytes")
+    if need > 0:
+        ws = _workspace(d, st, need)
+        L.workspace, L.workspace_bytes = ws.data_ptr(), ws.numel()
+    _lib.check(_lib.lib().dr_matmul(L), "dr_matmul")
+    del keep
+    return y
+
+
+def launch_plan(x, w, scale, **kw):
+    """What matmul(x, w, scale, **kw) launches, without launching it: {"kernel": "gemv" | "mfma", "rows_per_pass",
+    "tile_cols" (16 or 32), "tiles", "chunks", "kch", "splits", "workgroups", "passes", "records",
+    "tiles_per_record"} (the reference's choose/plan answer the same question for its Tensix split, linear.py:
+    455-495)."""
+    kw = dict(kw)
+    for knob in ("memory_config", "fidelity", "full_sync"):
+        kw.pop(knob, None)
+    L, _, keep = _launch(x, w, scale, **kw)
+    info = _lib.launch_info(L)
+    del keep
+    return info
+
+
+def _launch(x, w, scale, *, topk=None, out=None, col0=0, w_up=None, max_banks=None, **opts):
+    """matmul's checks (the reference's assertions), its dr_launch, y (allocated unless out is given), and the tensors
+    the launch points into that the caller does not hold (keep them alive until the launch is enqueued)."""
     d = x.device
     # weights sharded over more banks than allowed are refused before anything else (reference linear.py:627-633)
     if not isinstance(w, (list, tuple)):
@@ -488,15 +519,7 @@ def matmul(
         assert L.topk.slot0 + -(-n_out // TILE) <= L.topk.records_cap, (
             f"dense_reader: {-(-n_out // TILE)} records from slot {L.topk.slot0} do not fit {L.topk.records_cap}"
         )
-    st = torch.cuda.current_stream(d)
-    L.stream = st.cuda_stream
-    need = _lib.lib().dr_workspace_bytes(L)
-    _lib.check(_lib.DR_EINVAL if need < 0 else _lib.DR_OK, "dr_workspace_bytes")
-    if need > 0:
-        ws = _workspace(d, st, need)
-        L.workspace, L.workspace_bytes = ws.data_ptr(), ws.numel()
-    _lib.check(_lib.lib().dr_matmul(L), "dr_matmul")
-    return y
+    return L, y, (x2,)
 
 
 _WORKSPACE = {}

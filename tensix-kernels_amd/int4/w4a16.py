@@ -110,6 +110,25 @@ def w4a16_linear(x, wq, scale, *, memory_config=None, fidelity="hifi2", **opts):
 def rows_matmul(x2, wq, scale):
     """y [M, N] bf16 = x2 [M, K] (bf16, GPU) @ (q * s).T: dr_matmul with a DR_INT4 segment, any M (the library runs
     its GEMV two rows a pass)."""
+    L, y, x2 = _launch(x2, wq, scale)
+    need = _lib.lib().dr_workspace_bytes(L)
+    _lib.check(_lib.DR_EINVAL if need < 0 else _lib.DR_OK, "dr_workspace_bytes")
+    if need > 0:
+        ws = linear._workspace(x2.device, torch.cuda.current_stream(x2.device), need)
+        L.workspace, L.workspace_bytes = ws.data_ptr(), ws.numel()
+    _lib.check(_lib.lib().dr_matmul(L), "dr_matmul (int4)")
+    return y
+
+
+def launch_plan(x2, wq, scale):
+    """What rows_matmul(x2, wq, scale) launches (linear.launch_plan's dict), without launching it."""
+    L, _, x2 = _launch(x2, wq, scale)
+    return _lib.launch_info(L)
+
+
+def _launch(x2, wq, scale):
+    """rows_matmul's checks, its dr_launch (one DR_INT4 segment), y, and the contiguous x the launch reads (the
+    caller holds it until the launch is enqueued)."""
     n, k = wq["n"], wq["k"]
     assert x2.dim() == 2 and x2.shape[1] == k and x2.dtype == torch.bfloat16 and x2.is_cuda, (x2.shape, x2.dtype, k)
     assert (
@@ -131,13 +150,7 @@ def rows_matmul(x2, wq, scale):
     s0.codes, s0.exps = wq["t"].data_ptr(), None
     s0.scale = scale.data_ptr()
     L.stream = torch.cuda.current_stream(x2.device).cuda_stream
-    need = _lib.lib().dr_workspace_bytes(L)
-    _lib.check(_lib.DR_EINVAL if need < 0 else _lib.DR_OK, "dr_workspace_bytes")
-    if need > 0:
-        ws = linear._workspace(x2.device, torch.cuda.current_stream(x2.device), need)
-        L.workspace, L.workspace_bytes = ws.data_ptr(), ws.numel()
-    _lib.check(_lib.lib().dr_matmul(L), "dr_matmul (int4)")
-    return y
+    return L, y, x2
 
 
 def _codes_q(wq):

@@ -216,22 +216,80 @@ def test_block_list_bitwise(device):
 
 @pytest.mark.parametrize("fmt", ["bfp8", "bfp4", "bf16"])
 def test_narrow_tiles_bitwise(device, fmt):
-    """A launch of fewer 32-column tiles than the device has CUs runs 16-column tiles: the same columns inside a launch
-    of many tiles (a block list with a wide second block, 32-column tiles) are the same bit for bit, with scales and a
-    split K."""
+    """A launch of few 32-column tiles runs 16-column tiles (one panel a workgroup, so that every CU streams); the same
+    columns inside a launch of enough tiles for 32-column tiles (a block list whose second block brings the launch to
+    1.75 tiles a CU) are the same bit for bit, with fp32 scales and a split K. launch_plan names the width each runs."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
+    wide_tiles = 7 * cus // 4  # 448 on 256 CUs: two 32-column tiles a CU at most, the same as four halves
     for k in (2048, 9216):
         n = 1000
         tw, _ = linear.native_weight(device, matrix(n, k, 80), DTYPES[fmt])
-        big, _ = linear.native_weight(device, matrix(32 * cus, k, 81), DTYPES[fmt])
+        big, _ = linear.native_weight(device, matrix(32 * (wide_tiles - 32), k, 81), DTYPES[fmt])
         sc = linear.scale_tensor(device, torch.rand(n, generator=torch.Generator().manual_seed(82)) + 0.5,
                                  dtype=linear.float32)
         for m in (1, 2):
             x, tx = x_input(device, m, k, 83 + m)
+            narrow = linear.launch_plan(tx, tw, sc)
+            wide = linear.launch_plan(tx, [(tw, 0, sc), (big, 32)], None)
+            assert narrow["tile_cols"] == 16 and wide["tile_cols"] == 32, (narrow, wide)
+            assert narrow["kernel"] == wide["kernel"] == "gemv" and wide["tiles"] == wide_tiles, (narrow, wide)
             alone = host(linear.matmul(tx, tw, sc), m, n)
             check(f"{fmt} K {k} rows {m} narrow tiles", alone, ref(x, held(tw, n)) * sc.float().cpu().reshape(1, -1))
-            wide = linear.matmul(tx, [(tw, 0, sc), (big, 32)], None)
-            same(f"{fmt} K {k} rows {m} narrow against wide tiles", host(wide, m, n), alone)
+            both = linear.matmul(tx, [(tw, 0, sc), (big, 32)], None)
+            same(f"{fmt} K {k} rows {m} 16-column tiles against 32-column tiles", host(both, m, n), alone)
+
+
+def _edge_weights(k, exps, seed, every=1):
+    """[16 len(exps), k] weights at the ends of the shared-exponent range: in panel p (16 columns), at every `every`-th
+    k, the face row's 16 values are (1 + u) 2^(E - 127), u in [0, 1), random signs, E = exps[p] (the face row's shared
+    exponent); the other k hold N(0, 0.02). Column 3 at k = 1 is a denormal input (it rounds to zero)."""
+    n = 16 * len(exps)
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(n, k, generator=g) * 0.02
+    sel = torch.arange(0, k, every)
+    e = torch.tensor(exps, dtype=torch.float64).repeat_interleave(16)
+    mag = (1 + torch.rand(n, len(sel), generator=g, dtype=torch.float64)) * torch.exp2(e - 127)[:, None]
+    sign = torch.where(torch.rand(n, len(sel), generator=g) < 0.5, -1.0, 1.0).double()
+    w[:, sel] = (mag * sign).float()
+    w[3, 1] = 1e-40
+    return w, sel
+
+
+@pytest.mark.parametrize("fmt", ["bfp8", "bfp4"])
+@pytest.mark.parametrize("edge", ["low", "high"])
+def test_exponent_edges(device, fmt, edge):
+    """The exponent folding at the ends of the exponent range (moe8.py:147-149's zero / denormal rule): panels whose
+    face rows all have shared exponent E = 1 .. 10 (x 2^(E - bias) is an fp32 / bf16 denormal for the smallest), or
+    E = 245 .. 250 at every 128th k (x there +-1.5, so that the float64 result stays finite in fp32), through the GEMV
+    (rows 1, 2) and the MFMA decode (rows 3, 32), panel by panel against x @ held in float64."""
+    k = 1024
+    if edge == "low":
+        exps = [1, 2, 3, 4, 5, 6, 8, 10]
+        wt, sel = _edge_weights(k, exps, 300)
+    else:
+        exps = [245, 246, 247, 248, 249, 250]
+        wt, sel = _edge_weights(k, exps, 301, every=128)
+    n = wt.shape[0]
+    tw, _ = linear.native_weight(device, wt, DTYPES[fmt])
+    wk = held(tw, n)
+    same(f"{fmt} {edge} exponents: held values against the oracle", wk, torch.from_numpy(O.held(wt.T.contiguous(), fmt)))
+    assert bool(torch.isfinite(wk).all())
+    for m in (1, 2, 3, 32):
+        x = O.x_input(m, k, 302 + m)
+        if edge == "high":
+            x[:, sel] = torch.where(x[:, sel] < 0, -1.5, 1.5)
+        tx = x.to(torch.bfloat16).reshape(1, 1, m, k).to(device.torch)
+        y = host(linear.matmul(tx, tw, None), m, n)
+        want = ref(x, wk)
+        for p, e in enumerate(exps):
+            c = slice(16 * p, 16 * p + 16)
+            if fmt == "bfp4" and m <= 2 and e < 3:
+                # the bfloat4_b GEMV folds 2^(E - 129) into x as a bf16: below E + log2|x| = 3 that x' is a bf16
+                # denormal and keeps only its high bits (measured: 0.7 % at E = 2, 0.9-1.3 % at E = 1)
+                check(f"{fmt} rows {m} panel {p} shared exponent {e} (bf16-denormal x')", y[:, c], want[:, c],
+                      rel=0.03, pcc=0.9995)
+            else:
+                check(f"{fmt} rows {m} panel {p} shared exponent {e}", y[:, c], want[:, c])
 
 
 def test_max_banks(device):

@@ -52,9 +52,10 @@ def test_struct_layout_matches_c(tmp_path):
     src = tmp_path / "layout.c"
     src.write_text(
         '#include <stdio.h>\n#include <stddef.h>\n#include "dense_reader.h"\n'
-        "int main(void){printf(\"%zu %zu %zu %zu %zu %zu %zu %zu %zu\\n\", sizeof(dr_segment), sizeof(dr_topk),"
+        "int main(void){printf(\"%zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\\n\", sizeof(dr_segment), sizeof(dr_topk),"
         " sizeof(dr_launch), offsetof(dr_launch, seg), offsetof(dr_launch, topk), offsetof(dr_launch, stream),"
-        " offsetof(dr_topk, base), offsetof(dr_segment, col0), offsetof(dr_launch, workspace_bytes));return 0;}\n"
+        " offsetof(dr_topk, base), offsetof(dr_segment, col0), offsetof(dr_launch, workspace_bytes),"
+        " sizeof(dr_launch_info), offsetof(dr_launch_info, tiles_per_record));return 0;}\n"
     )
     exe = tmp_path / "layout"
     subprocess.run(["gcc", "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
@@ -69,6 +70,8 @@ def test_struct_layout_matches_c(tmp_path):
         _lib.TopK.base.offset,
         _lib.Segment.col0.offset,
         _lib.Launch.workspace_bytes.offset,
+        ctypes.sizeof(_lib.LaunchInfo),
+        _lib.LaunchInfo.tiles_per_record.offset,
     ]
     assert got == want
 
@@ -117,6 +120,29 @@ def test_invalid_arguments_refused_on_the_host():
         _lib.check(_lib.DR_EINVAL, "x")
     with pytest.raises(RuntimeError):
         _lib.check(_lib.DR_EHIP, "x")
+
+
+def _ns_launch(m=1, k=4096, n=14336, fmt=0):
+    L = _lib.Launch()  # device pointers that are never read: the plan only reads the launch's sizes
+    L.x, L.y, L.m, L.k, L.ldx, L.ldy, L.nseg = 16, 16, m, k, k, n, 1
+    s = L.seg[0]
+    s.fmt, s.n, s.n_pad, s.codes, s.exps = fmt, n, -(-n // 32) * 32, 16, 16
+    return L
+
+
+def test_launch_plan_on_the_host():
+    """dr_launch_plan answers without a device (as if it had 256 CUs): the north star on the wide GEMV, 32 rows on the
+    MFMA kernel, a long K split, top-k records one a tile; an invalid launch is refused."""
+    p = _lib.launch_info(_ns_launch())
+    assert (p["kernel"], p["rows_per_pass"], p["tile_cols"], p["tiles"], p["splits"]) == ("gemv", 1, 32, 448, 1), p
+    p = _lib.launch_info(_ns_launch(m=32))
+    assert (p["kernel"], p["rows_per_pass"], p["passes"]) == ("mfma", 32, 1), p
+    p = _lib.launch_info(_ns_launch(m=8, k=14336, n=4096))
+    assert (p["kernel"], p["rows_per_pass"], p["splits"], p["chunks"], p["kch"]) == ("mfma", 16, 2, 28, 512), p
+    p = _lib.launch_info(_ns_launch(n=1000))
+    assert (p["tile_cols"], p["tiles"]) == (16, 63), p  # few tiles: 16-column tiles
+    info = _lib.LaunchInfo()
+    assert _lib.lib().dr_launch_plan(ctypes.byref(_lib.Launch()), ctypes.byref(info)) == _lib.DR_EINVAL
 
 
 class _FakeWeight:

@@ -133,6 +133,10 @@ typedef struct dr_launch {
     void* stream;        /* hipStream_t */
 } dr_launch;
 
+/* dr_matmul_noalloc's own device workspace: DR_SCRATCH_BYTES a GPU, from the first call on a device until the process
+ * ends. */
+#define DR_SCRATCH_BYTES (8 << 20)
+
 /* Bytes of workspace the launch needs (0: none; a K long enough to split over several workgroups a tile needs some;
  * -1: the launch is invalid). The workspace is zeroed once when allocated; every launch leaves its counters at zero,
  * and they lie at the same place whatever the launch's shape, so launches of any shape (dr_matmul's and
@@ -143,6 +147,16 @@ int64_t dr_workspace_bytes(const dr_launch* launch);
 /* y = the launch's fused matmul. Allocates nothing. A DR_INT4 weight goes alone (one segment, no GLU, residual or
  * top-k) and takes its rows two at a time (int4/w4a16.py:170-253 w4a16_linear takes one token). */
 int dr_matmul(const dr_launch* launch);
+
+/* dr_matmul without a caller workspace: a launch that needs one (dr_workspace_bytes > 0) uses the library's own,
+ * a static device array of DR_SCRATCH_BYTES on each GPU (dr_scratch_bytes), so the call allocates nothing and needs
+ * nothing but the launch's inputs and outputs. No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). A
+ * launch that needs more than DR_SCRATCH_BYTES is refused (DR_ERANGE) before anything is enqueued. Every call on one
+ * GPU shares that GPU's array (calls that overlap in time on one GPU race: keep them on one stream); the first call on
+ * a device enqueues a fill of its counters on the launch's stream. */
+int dr_matmul_noalloc(const dr_launch* launch);
+int64_t dr_scratch_bytes(void);
 
 /* The best k_out of records [n_records][2 * rows * k] (as dr_topk writes them) per row: vals [rows][k_out] fp32
  * (-inf empty), ids [rows][k_out] int32 (-1 empty), highest first, ties to the lower id. rows <= 32 (a record's, as

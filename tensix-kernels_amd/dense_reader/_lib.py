@@ -24,6 +24,8 @@ SYMBOLS = (
     "dr_pack_int4_scales",
     "dr_unpack",
     "dr_matmul",
+    "dr_matmul_noalloc",
+    "dr_scratch_bytes",
     "dr_workspace_bytes",
     "dr_topk_merge",
     "dr_topk_merge_workspace_bytes",
@@ -188,6 +190,10 @@ def lib():
         L.dr_unpack.argtypes = [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_int64, c_void_p]
         L.dr_matmul.restype = c_int
         L.dr_matmul.argtypes = [ctypes.POINTER(Launch)]
+        L.dr_matmul_noalloc.restype = c_int
+        L.dr_matmul_noalloc.argtypes = [ctypes.POINTER(Launch)]
+        L.dr_scratch_bytes.restype = c_int64
+        L.dr_scratch_bytes.argtypes = []
         L.dr_workspace_bytes.restype = c_int64
         L.dr_workspace_bytes.argtypes = [ctypes.POINTER(Launch)]
         L.dr_topk_merge.restype = c_int

@@ -26,6 +26,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <mutex>
 #include <stdint.h>
 
 #include "dense_reader.h"
@@ -2265,6 +2266,57 @@ void bind_split(Args& a, void* workspace) {
     a.wpart = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + (int64_t)SPLIT_MAXTILES * 4);
 }
 
+// dr_matmul's launches: one pass of up to mr rows each (the passes a top-k launch needs, not y, skipped)
+int run_passes(const dr_launch* L, const Args& a, int tiles, int mr, int pw, hipStream_t st) {
+    const size_t ysz = a.y_f32 ? 4 : 2;
+    for (int r0 = 0; r0 < L->m; r0 += mr) {
+        Args p = a;
+        p.m = L->m - r0 < mr ? L->m - r0 : mr;
+        p.x = a.x + (size_t)r0 * a.ldx;
+        p.y = reinterpret_cast<uint8_t*>(L->y) + (size_t)r0 * a.ldy * ysz;
+        if (a.res) p.res = a.res + (size_t)r0 * a.ldr;
+        p.row0 = r0;
+        if (a.rec != nullptr && r0 >= a.tk_rows && !a.write_y) continue;
+        const hipError_t e = launch_rows(p, mr, pw, tiles * a.splits, st);
+        if (e != hipSuccess) return DR_EHIP;
+    }
+    return DR_OK;
+}
+
+// ---- the library's own workspace, for dr_matmul_noalloc ---------------------------------------------------------------
+//
+// A file-scope device array, one copy on every GPU the library runs on, held until the process ends. Host code never
+// uses its name as an address (on the host it is only a stand-in for the symbol): each device's address comes from
+// hipGetSymbolAddress, once per device with that device current, and that address is what kernels and fills get.
+// It serves as dr_matmul's workspace: the split-K counters must start at zero (a fill kernel clears them on a device's
+// first call; every launch leaves them at zero), the partial sums need no clearing.
+static __device__ __align__(256) uint8_t scratch[DR_SCRATCH_BYTES];
+
+__global__ __launch_bounds__(256) void dr_zero_k(uint32_t* __restrict__ p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+constexpr int SCRATCH_DEVICES = 64;
+std::mutex scratch_mu;
+void* scratch_addr[SCRATCH_DEVICES];  // (guarded by scratch_mu)
+
+// the current device's scratch address (its counters cleared on first use, on `st`), or null on a HIP error
+void* scratch_for_current_device(hipStream_t st) {
+    int d = 0;
+    if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= SCRATCH_DEVICES) return nullptr;
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (scratch_addr[d] == nullptr) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) return nullptr;
+        constexpr int n = SPLIT_MAXTILES;  // the counters: the first SPLIT_MAXTILES words
+        hipLaunchKernelGGL(dr_zero_k, dim3((n + 255) / 256), dim3(256), 0, st, reinterpret_cast<uint32_t*>(ptr), n);
+        if (hipGetLastError() != hipSuccess) return nullptr;
+        scratch_addr[d] = ptr;
+    }
+    return scratch_addr[d];
+}
+
 
 }  // namespace
 
@@ -2291,20 +2343,26 @@ int dr_matmul(const dr_launch* L) {
         if (L->workspace == nullptr || L->workspace_bytes < need) return DR_EINVAL;
         bind_split(a, L->workspace);
     }
+    return run_passes(L, a, tiles, mr, pw, S(L->stream));
+}
+
+int64_t dr_scratch_bytes(void) { return DR_SCRATCH_BYTES; }
+
+int dr_matmul_noalloc(const dr_launch* L) {
+    Args a{};
+    int pw, tiles, mr;
+    if (L != nullptr && L->act == DR_ACT_SWIGLU_OAI) return DR_EINVAL;
+    const int st0 = prepare(L, a, pw, tiles, mr);
+    if (st0 != DR_OK) return st0;
+    const int64_t need = workspace_bytes(a, pw, mr);
+    if (need > DR_SCRATCH_BYTES) return DR_ERANGE;  // (checked before any device call)
     hipStream_t st = S(L->stream);
-    const size_t ysz = a.y_f32 ? 4 : 2;
-    for (int r0 = 0; r0 < L->m; r0 += mr) {
-        Args p = a;
-        p.m = L->m - r0 < mr ? L->m - r0 : mr;
-        p.x = a.x + (size_t)r0 * a.ldx;
-        p.y = reinterpret_cast<uint8_t*>(L->y) + (size_t)r0 * a.ldy * ysz;
-        if (a.res) p.res = a.res + (size_t)r0 * a.ldr;
-        p.row0 = r0;
-        if (a.rec != nullptr && r0 >= a.tk_rows && !a.write_y) continue;
-        const hipError_t e = launch_rows(p, mr, pw, tiles * a.splits, st);
-        if (e != hipSuccess) return DR_EHIP;
+    if (need > 0) {
+        void* ws = scratch_for_current_device(st);
+        if (ws == nullptr) return DR_EHIP;
+        bind_split(a, ws);
     }
-    return DR_OK;
+    return run_passes(L, a, tiles, mr, pw, st);
 }
 
 int dr_launch_plan(const dr_launch* L, dr_launch_info* info) {

@@ -193,7 +193,8 @@ class Workload:
         n = self.n
         self.res = torch.randn(m, n, generator=g, device="cuda").to(torch.bfloat16).reshape(1, 1, m, n) if o.get("residual") else None
         self.y = torch.empty(1, 1, m, n, dtype=torch.bfloat16, device="cuda")
-        self.rec = linear.topk_result(dev, linear.topk_slots(n), m, 8) if o.get("topk") else None
+        # (c5: a record per 32-column block, as the config asks: no limit on the records)
+        self.rec = linear.topk_result(dev, linear.topk_slots(n, 0), m, 8) if o.get("topk") else None
         self.col0 = []
         c = 0
         for nb, _, _ in ws:
@@ -250,7 +251,8 @@ class Workload:
             blocks = [(w, c0, s) if s is not None else (w, c0) for w, c0, s in zip(ws, self.col0, self.scales)]
             L.matmul(self.x, blocks, None, out=self.y)
         elif o.get("topk"):
-            spec = {"r": self.rec, "k": 8, "rows": self.m, "slot0": 0, "base": 0, "n": self.n, "write_y": False, "fp32": True}
+            spec = {"r": self.rec, "k": 8, "rows": self.m, "slot0": 0, "base": 0, "n": self.n, "write_y": False,
+                    "fp32": True, "slots": 0}
             L.matmul(self.x, ws[0], None, out=self.y, topk=spec)
         elif o.get("lmhead"):
             h = self.heads[i % self.copies]

@@ -98,11 +98,15 @@ typedef struct dr_segment {
     int32_t col0;         /* first output column in y, a multiple of 32 */
 } dr_segment;
 
-/* Top-k records: for every 32-column output tile t of the launch, one record at index slot0 + t holding, for each
- * of the first `rows` rows, the best k values of that tile (highest first, ties to the lower column), written as
- * rows * k keys then rows * k ids (uint32 words). fp32 0: keys are the reference's bf16 keys of the bf16 output
- * (0 empty) and ids base + column (0xFFFFFFFF empty); fp32 1: keys are the fp32 scores' bits (-inf empty) and ids
- * int32 (-1 empty). */
+/* Top-k records: the launch's 32-column output tiles in groups of G consecutive tiles, one record for each group at
+ * index slot0 + group, holding, for each of the first `rows` rows, the best k values of the group's columns (highest
+ * first, ties to the lower column), written as rows * k keys then rows * k ids (uint32 words). G = 1 (a record a
+ * tile) unless the launch has more tiles than max_records; then G = ceil(tiles / max_records), so that a launch
+ * writes at most max_records records, as the reference's writes at most one a core of its grid (a caller that sizes
+ * each block's records by the grid's cores, lm_head_topk/lmhead.py:102-103, stays within them). fp32 0: keys are the
+ * reference's bf16 keys of the bf16 output (0 empty) and ids base + column (0xFFFFFFFF empty); fp32 1: keys are the
+ * fp32 scores' bits (-inf empty) and ids int32 (-1 empty). Grouped launches (G > 1) need the workspace
+ * (dr_workspace_bytes) and at most 1024 = G * k candidates a row and 4096 records. */
 typedef struct dr_topk {
     void* records;       /* [records_cap][2 * rows * k] uint32, or NULL: no top-k */
     int32_t k;           /* 1 .. 32 */
@@ -113,6 +117,7 @@ typedef struct dr_topk {
     int64_t base;        /* id of output column 0 */
     int32_t write_y;     /* 0: y is not written */
     int32_t fp32;
+    int32_t max_records; /* records the launch writes at most (the caller's records per block); 0: one a tile */
 } dr_topk;
 
 typedef struct dr_launch {

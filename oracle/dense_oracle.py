@@ -331,19 +331,20 @@ def key_value(keys):
     return bf16_values(bits.astype(np.uint32))
 
 
-def tile_topk(y, rows, k, n_valid, base, fp32=False, yf=None):
+def tile_topk(y, rows, k, n_valid, base, fp32=False, yf=None, width=32):
     """The records this build writes for output y [M, N] (bf16 values as float32; yf: the fp32 scores when fp32):
-    per 32-column tile t, per row r < rows, the best k of columns [32t, 32t + 32) below n_valid, highest first, ties
-    to the lower column. Returns uint32 words [tiles, 2 * rows * k]: keys then ids (bf16 keys 0 / ids 0xFFFFFFFF
-    empty; fp32: score bits, -inf / 0xFFFFFFFF empty)."""
+    per `width` columns (a 32-column tile, or a group of tiles; the reference's writer ranks each core's columns
+    together, dense_writer.cpp:185-232), per row r < rows, the best k of columns [width t, width t + width) below
+    n_valid, highest first, ties to the lower column. Returns uint32 words [records, 2 * rows * k]: keys then ids (bf16
+    keys 0 / ids 0xFFFFFFFF empty; fp32: score bits, -inf / 0xFFFFFFFF empty)."""
     y = np.asarray(y, np.float32)
     M, N = y.shape
-    tiles = -(-N // 32)
+    tiles = -(-N // width)
     out = np.zeros((tiles, 2, rows, k), np.uint64)
     for t in range(tiles):
         for r in range(rows):
             cand = []
-            for c in range(32 * t, min(32 * t + 32, N)):
+            for c in range(width * t, min(width * t + width, N)):
                 if c >= n_valid:
                     continue
                 if fp32:

@@ -74,6 +74,7 @@ class TopK(ctypes.Structure):
         ("base", c_int64),
         ("write_y", c_int32),
         ("fp32", c_int32),
+        ("max_records", c_int32),
     ]
 
 

@@ -108,6 +108,9 @@ struct Args {
     SegDev seg[4];
     uint32_t* rec;
     int tk_k, tk_rows, slot0, n_valid, write_y, tk_fp32, row0;
+    int tk_group;            // tiles a record (> 1: each tile's record is staged in tstage, its group's last merges)
+    uint32_t* gcounters;     // [records] (tk_group > 1): tiles of the group done, reset to 0 by the last
+    uint32_t* tstage;        // [tiles][2 * rows * k] (tk_group > 1): each tile's record
     long long base;
     int chunks, kch, waves;
     int splits, cps, tiles;  // split K: splits workgroups a tile, cps chunks each; tiles of the launch
@@ -667,6 +670,69 @@ __device__ __forceinline__ uint32_t key_f32(float f) {
     return u ^ ((u >> 31) ? 0xFFFFFFFFu : 0x80000000u);
 }
 
+// ---- top-k records of tile groups ------------------------------------------------------------------------------------
+//
+// A launch with more tiles than the caller's records writes one record a group of tk_group consecutive tiles (the
+// reference writes one a core, each core's columns ranked together, dense_writer.cpp:185-232). Every tile ranks its
+// own 32 columns into a staging record (device-scope stores), waits for them, and counts itself on its group's
+// counter; the group's last tile reads the group's staged records (device-scope loads) and ranks their candidates by
+// a 64-bit key, the record's key above the id complemented (0 empty), so the order is the tiles' own: highest first,
+// ties to the lower id. It writes the group's record and resets the counter. The device-scope accesses meet at the
+// device's point of coherence as split K's do (the XCDs' L2 caches are not coherent with each other).
+
+__device__ __forceinline__ unsigned long long cand_key(uint32_t word, uint32_t id, bool fp32) {
+    if (id == 0xFFFFFFFFu || (!fp32 && word == 0u)) return 0ull;
+    const uint32_t ok = fp32 ? key_f32(__uint_as_float(word)) : word;
+    return ((unsigned long long)ok << 32) | (unsigned long long)(0xFFFFFFFFu - id);
+}
+
+// cand: LDS of at least 2 * tk_group * tk_k words (the launch's dynamic LDS is sized for it)
+__device__ __forceinline__ void topk_group_merge(const Args& a, int t, uint32_t* cand, int mrows) {
+    __shared__ int last;
+    const int G = a.tk_group, K = a.tk_k, R = a.tk_rows;
+    const int grp = t / G, t0 = grp * G, members = min(G, a.tiles - t0);
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's staging stores have reached the point of coherence
+    __syncthreads();
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(a.gcounters + grp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               (uint32_t)(members - 1);
+    __syncthreads();
+    if (!last) return;
+    const size_t rlen = 2 * (size_t)R * K;
+    const int n = members * K;
+    const bool fp32 = a.tk_fp32 != 0;
+    uint32_t* out = a.rec + (size_t)(a.slot0 + grp) * rlen;
+    for (int m = 0; m < mrows; ++m) {
+        const int r = a.row0 + m;
+        if (r >= R) break;
+        for (int i = threadIdx.x; i < n; i += blockDim.x) {
+            const uint32_t* src = a.tstage + (size_t)(t0 + i / K) * rlen + (size_t)r * K + i % K;
+            cand[i] = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            cand[n + i] = __hip_atomic_load(src + (size_t)R * K, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        for (int i = threadIdx.x; i < n; i += blockDim.x) {
+            const unsigned long long ci = cand_key(cand[i], cand[n + i], fp32);
+            int rank = 0, nval = 0;
+            for (int j = 0; j < n; ++j) {
+                const unsigned long long cj = cand_key(cand[j], cand[n + j], fp32);
+                rank += cj > ci;
+                nval += cj != 0ull;
+            }
+            if (ci != 0ull && rank < K) {
+                out[(size_t)r * K + rank] = cand[i];
+                out[(size_t)R * K + (size_t)r * K + rank] = cand[n + i];
+            }
+            if (i < K && i >= nval) {
+                out[(size_t)r * K + i] = fp32 ? 0xFF800000u : 0u;
+                out[(size_t)R * K + (size_t)r * K + i] = 0xFFFFFFFFu;
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(a.gcounters + grp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ---- expert gather: ids, the union of the rows' ids ----------------------------------------------------------------
 
 // expert id j of row r, or -1 when it is not below the expert count (it chooses nothing)
@@ -833,11 +899,19 @@ __device__ __forceinline__ void epilogue(const Args& a, const SegDev& sg, int t,
     }
     if (!topk) return;
     __syncthreads();
-    // one wavefront ranks each row's 32 keys: the best k, highest first, ties to the lower column
+    const bool grouped = a.tk_group > 1;
+    // one wavefront ranks each row's 32 keys: the best k, highest first, ties to the lower column. The record goes to
+    // its slot, or (grouped) to the tile's staging slot, with device-scope stores that the group's last tile reads.
     if (wave == 0) {
         const int K = a.tk_k, R = a.tk_rows;
         const size_t rlen = 2 * (size_t)R * K;
-        uint32_t* rec = a.rec + (size_t)(a.slot0 + t) * rlen;
+        uint32_t* rec = grouped ? a.tstage + (size_t)t * rlen : a.rec + (size_t)(a.slot0 + t) * rlen;
+        auto put = [grouped](uint32_t* p, uint32_t v) {
+            if (grouped)
+                __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else
+                *p = v;
+        };
         for (int m = 0; m < mrows; ++m) {
             const int r = a.row0 + m;
             if (r >= R) break;
@@ -851,15 +925,16 @@ __device__ __forceinline__ void epilogue(const Args& a, const SegDev& sg, int t,
             }
             if (lane < 32 && key != 0u && rank < K) {
                 const float val = tval[m][c];
-                rec[(size_t)r * K + rank] = a.tk_fp32 ? __float_as_uint(val) : key;
-                rec[(size_t)R * K + (size_t)r * K + rank] = (uint32_t)(a.base + (long long)t * TILE + c);
+                put(rec + (size_t)r * K + rank, a.tk_fp32 ? __float_as_uint(val) : key);
+                put(rec + (size_t)R * K + (size_t)r * K + rank, (uint32_t)(a.base + (long long)t * TILE + c));
             }
             if (lane >= nval && lane < K) {
-                rec[(size_t)r * K + lane] = a.tk_fp32 ? 0xFF800000u : 0u;
-                rec[(size_t)R * K + (size_t)r * K + lane] = 0xFFFFFFFFu;
+                put(rec + (size_t)r * K + lane, a.tk_fp32 ? 0xFF800000u : 0u);
+                put(rec + (size_t)R * K + (size_t)r * K + lane, 0xFFFFFFFFu);
             }
         }
     }
+    if (grouped) topk_group_merge(a, t, reinterpret_cast<uint32_t*>(const_cast<float*>(part)), mrows);
 }
 
 // the gate/up modes' epilogue: thread (m, col) of the tile adds the bias, applies the GLU and the row's routing weight
@@ -934,6 +1009,8 @@ __device__ __forceinline__ void moe_zero(const MoeArgs& a, int t, int unit) {
 #define DR_SPLIT_MAXTILES 16384
 #endif
 constexpr int SPLIT_MAXTILES = DR_SPLIT_MAXTILES;  // counters in the workspace: tiles of a split launch at most
+constexpr int GROUP_MAXRECORDS = 4096;  // record-group counters in the workspace: records of a grouped launch at most
+constexpr int GROUP_MAXCAND = 1024;     // candidates a row of a grouped record at most (tiles a record x k)
 
 __device__ __forceinline__ void st_dev(float* p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1948,10 +2025,17 @@ int rows_per_pass(int m) {
     return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
 }
 
+// dynamic LDS of a dense launch: the partial sums, or a grouped record's candidates (2 * tiles a record * k words)
+size_t dense_lds(const Args& a, int pw, int rows) {
+    const size_t sums = (size_t)max(a.waves, a.splits) * pw * rows * 16 * sizeof(float);
+    const size_t cand = a.rec != nullptr && a.tk_group > 1 ? (size_t)2 * a.tk_group * a.tk_k * sizeof(uint32_t) : 0;
+    return max(sums, cand);
+}
+
 template <int MR, int PW>
 void launch_gemv(const Args& a, int grid, hipStream_t st) {
     const dim3 b(64 * a.waves);
-    const size_t lds = (size_t)max(a.waves, a.splits) * PW * MR * 16 * sizeof(float);
+    const size_t lds = dense_lds(a, PW, MR);
     if (a.nseg > 1) {
         hipLaunchKernelGGL((dr_gemv<MR, PW, -1, false>), dim3(grid), b, lds, st, a);
         return;
@@ -1969,7 +2053,7 @@ void launch_gemv(const Args& a, int grid, hipStream_t st) {
 template <int MT, int PW>
 void launch_mfma(const Args& a, int grid, hipStream_t st) {
     const dim3 b(64 * a.waves);
-    const size_t lds = (size_t)max(a.waves, a.splits) * PW * 16 * MT * 16 * sizeof(float);
+    const size_t lds = dense_lds(a, PW, 16 * MT);
     if (a.nseg > 1) {
         hipLaunchKernelGGL((dr_mfma<MT, PW, -1, false>), dim3(grid), b, lds, st, a);
         return;
@@ -2217,10 +2301,16 @@ int prepare(const dr_launch* L, Args& a, int& pw, int& tiles, int& mr, bool gath
     if (a.res != nullptr && (L->ldr < a.seg[0].col0 + a.seg[0].n_out || L->nseg != 1 || pw != 2)) return DR_EINVAL;
     const dr_topk& T = L->topk;
     a.rec = reinterpret_cast<uint32_t*>(T.records);
+    a.tk_group = 1;
     if (a.rec != nullptr) {
         if (T.k < 1 || T.k > 32 || T.rows < 1 || T.rows > 32 || T.rows > L->m || T.slot0 < 0 || L->nseg != 1 ||
-            pw != 2 || T.slot0 + tiles > T.records_cap || T.n_valid < 0)
+            pw != 2 || T.n_valid < 0 || T.max_records < 0)
             return DR_EINVAL;
+        // tiles in groups so that the launch writes at most max_records records
+        if (T.max_records > 0 && tiles > T.max_records) a.tk_group = (tiles + T.max_records - 1) / T.max_records;
+        const int records = (tiles + a.tk_group - 1) / a.tk_group;
+        if ((int64_t)T.slot0 + records > T.records_cap) return DR_EINVAL;
+        if (a.tk_group > 1 && (a.tk_group * T.k > GROUP_MAXCAND || records > GROUP_MAXRECORDS)) return DR_ERANGE;
         a.tk_k = T.k;
         a.tk_rows = T.rows;
         a.slot0 = T.slot0;
@@ -2255,15 +2345,27 @@ int prepare(const dr_launch* L, Args& a, int& pw, int& tiles, int& mr, bool gath
     return DR_OK;
 }
 
-// split K's workspace: SPLIT_MAXTILES counters, then every workgroup's column sums
-int64_t workspace_bytes(const Args& a, int pw, int mr) {
-    if (a.splits == 1) return 0;
-    return (int64_t)SPLIT_MAXTILES * 4 + (int64_t)a.tiles * a.splits * pw * mr * 16 * 4;
+// The workspace: SPLIT_MAXTILES split-K counters and GROUP_MAXRECORDS record-group counters at fixed places (so that
+// launches of any shape can share one), then split K's column sums (every workgroup's), then the grouped records'
+// staging (every tile's record).
+constexpr int64_t WS_COUNTERS = ((int64_t)SPLIT_MAXTILES + GROUP_MAXRECORDS) * 4;
+
+int64_t split_sums_bytes(const Args& a, int pw, int mr) {
+    return a.splits > 1 ? (int64_t)a.tiles * a.splits * pw * mr * 16 * 4 : 0;
 }
 
-void bind_split(Args& a, void* workspace) {
-    a.counters = reinterpret_cast<uint32_t*>(workspace);
-    a.wpart = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + (int64_t)SPLIT_MAXTILES * 4);
+int64_t workspace_bytes(const Args& a, int pw, int mr) {
+    if (a.splits == 1 && a.tk_group <= 1) return 0;
+    const int64_t stage = a.tk_group > 1 ? (int64_t)a.tiles * 2 * a.tk_rows * a.tk_k * 4 : 0;
+    return WS_COUNTERS + split_sums_bytes(a, pw, mr) + stage;
+}
+
+void bind_split(Args& a, void* workspace, int pw, int mr) {
+    uint8_t* w = reinterpret_cast<uint8_t*>(workspace);
+    a.counters = reinterpret_cast<uint32_t*>(w);
+    a.gcounters = reinterpret_cast<uint32_t*>(w + (int64_t)SPLIT_MAXTILES * 4);
+    a.wpart = reinterpret_cast<float*>(w + WS_COUNTERS);
+    a.tstage = reinterpret_cast<uint32_t*>(w + WS_COUNTERS + split_sums_bytes(a, pw, mr));
 }
 
 // dr_matmul's launches: one pass of up to mr rows each (the passes a top-k launch needs, not y, skipped)
@@ -2288,8 +2390,9 @@ int run_passes(const dr_launch* L, const Args& a, int tiles, int mr, int pw, hip
 // A file-scope device array, one copy on every GPU the library runs on, held until the process ends. Host code never
 // uses its name as an address (on the host it is only a stand-in for the symbol): each device's address comes from
 // hipGetSymbolAddress, once per device with that device current, and that address is what kernels and fills get.
-// It serves as dr_matmul's workspace: the split-K counters must start at zero (a fill kernel clears them on a device's
-// first call; every launch leaves them at zero), the partial sums need no clearing.
+// It serves as dr_matmul's workspace: the counters (split K's and the record groups') must start at zero (a fill kernel
+// clears them on a device's first call; every launch leaves them at zero), the partial sums and staging need no
+// clearing.
 static __device__ __align__(256) uint8_t scratch[DR_SCRATCH_BYTES];
 
 __global__ __launch_bounds__(256) void dr_zero_k(uint32_t* __restrict__ p, int n) {
@@ -2309,7 +2412,7 @@ void* scratch_for_current_device(hipStream_t st) {
     if (scratch_addr[d] == nullptr) {
         void* ptr = nullptr;
         if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) return nullptr;
-        constexpr int n = SPLIT_MAXTILES;  // the counters: the first SPLIT_MAXTILES words
+        constexpr int n = (int)(WS_COUNTERS / 4);  // the counters: split K's, then the record groups
         hipLaunchKernelGGL(dr_zero_k, dim3((n + 255) / 256), dim3(256), 0, st, reinterpret_cast<uint32_t*>(ptr), n);
         if (hipGetLastError() != hipSuccess) return nullptr;
         scratch_addr[d] = ptr;
@@ -2341,7 +2444,7 @@ int dr_matmul(const dr_launch* L) {
         // split K needs the workspace: its counters start at zero (the caller zeroes it once; each launch leaves
         // them at zero)
         if (L->workspace == nullptr || L->workspace_bytes < need) return DR_EINVAL;
-        bind_split(a, L->workspace);
+        bind_split(a, L->workspace, pw, mr);
     }
     return run_passes(L, a, tiles, mr, pw, S(L->stream));
 }
@@ -2360,7 +2463,7 @@ int dr_matmul_noalloc(const dr_launch* L) {
     if (need > 0) {
         void* ws = scratch_for_current_device(st);
         if (ws == nullptr) return DR_EHIP;
-        bind_split(a, ws);
+        bind_split(a, ws, pw, mr);
     }
     return run_passes(L, a, tiles, mr, pw, st);
 }
@@ -2385,8 +2488,8 @@ int dr_launch_plan(const dr_launch* L, dr_launch_info* info) {
     for (int r0 = 0; r0 < L->m; r0 += mr)
         if (!(a.rec != nullptr && r0 >= a.tk_rows && !a.write_y)) ++passes;
     info->passes = passes;
-    info->records = a.rec != nullptr ? tiles : 0;
-    info->tiles_per_record = a.rec != nullptr ? 1 : 0;
+    info->records = a.rec != nullptr ? (tiles + a.tk_group - 1) / a.tk_group : 0;
+    info->tiles_per_record = a.rec != nullptr ? a.tk_group : 0;
     return DR_OK;
 }
 
@@ -2550,7 +2653,7 @@ int dr_moe_matmul(const dr_launch* L, const dr_moe* M) {
     const int64_t need = workspace_bytes(a, pw, mr);
     if (need > 0) {
         if (L->workspace == nullptr || L->workspace_bytes < need) return DR_EINVAL;
-        bind_split(a, L->workspace);
+        bind_split(a, L->workspace, pw, mr);
     }
     hipStream_t st = S(L->stream);
     const size_t ysz = a.y_f32 ? 4 : 2;
@@ -2584,7 +2687,7 @@ int dr_moe_route_gate_up(const dr_launch* L, const dr_moe* M, const dr_route* R)
     const int64_t need = workspace_bytes(a, pw, mr);
     if (need > 0) {
         if (L->workspace == nullptr || L->workspace_bytes < need) return DR_EINVAL;
-        bind_split(a, L->workspace);
+        bind_split(a, L->workspace, pw, mr);
     }
     const hipError_t e = launch_moe(a, M->mode, mr, pw, tiles * a.splits, S(L->stream));
     return e == hipSuccess ? DR_OK : DR_EHIP;

@@ -367,10 +367,12 @@ def matmul(
     max_banks: refuse a weight sharded over more banks (default common.device.MAX_BANKS; None: no limit).
 
     topk (M <= 32): {"r": result tensor (topk_result), "k": K <= 32, "rows": T <= 32, "slot0": first record, "base":
-    index of output element 0, "n": valid output elements, "write_y": bool, "fp32": bool}: every 32-column output
-    tile writes one record, slot0 + its tile index, of each of the first T rows' best K values (keys, then ids;
-    topk_records decodes them). fp32 False (default): the reference's bf16 keys of the bf16 output; True: fp32 scores
-    (beyond the reference). y is still written with write_y. out: a [1, 1, M, N] tensor to write into instead of a new
+    index of output element 0, "n": valid output elements, "write_y": bool, "fp32": bool, "slots": records at most}:
+    every 32-column output tile writes one record, slot0 + its tile index, of each of the first T rows' best K values
+    (keys, then ids; topk_records decodes them); a launch of more tiles than "slots" (default grid_slots(), the
+    reference's records per block; 0: no limit) writes one record a group of consecutive tiles instead, so that it
+    writes at most "slots" (topk_slots gives the count). fp32 False (default): the reference's bf16 keys of the bf16
+    output; True: fp32 scores (beyond the reference). y is still written with write_y. out: a [1, 1, M, N] tensor to write into instead of a new
     one. col0 (with out, no topk): out is wider, [1, 1, M, W], and output column tile c goes to its tile c + col0.
 
     Options (opts): glu (the weight is interleave_glu's [gate | up], output act(gate) * up, N / 2 wide), glu_act (0
@@ -516,8 +518,11 @@ def _launch(x, w, scale, *, topk=None, out=None, col0=0, w_up=None, max_banks=No
         L.topk.base = topk.get("base", 0)
         L.topk.write_y = int(bool(topk.get("write_y", False)))
         L.topk.fp32 = int(bool(topk.get("fp32", False)))
-        assert L.topk.slot0 + -(-n_out // TILE) <= L.topk.records_cap, (
-            f"dense_reader: {-(-n_out // TILE)} records from slot {L.topk.slot0} do not fit {L.topk.records_cap}"
+        slots = topk.get("slots")
+        L.topk.max_records = grid_slots() if slots is None else int(slots)
+        records = topk_slots(n_out, L.topk.max_records)
+        assert L.topk.slot0 + records <= L.topk.records_cap, (
+            f"dense_reader: {records} records from slot {L.topk.slot0} do not fit {L.topk.records_cap}"
         )
     return L, y, (x2,)
 
@@ -587,9 +592,22 @@ def linear(x, w, scale, memory_config=None, activation=None, out_dtype=None, **o
 # --- top-k records ----------------------------------------------------------------------------------------------------
 
 
-def topk_slots(n):
-    """Records a top-k call over n output columns writes (one a 32-column tile)."""
-    return -(-n // TILE)
+def grid_slots():
+    """Records a top-k launch writes at most by default: the cores of the device's grid
+    (compute_with_storage_grid_size), as the reference writes one a core of its plan and its callers size a block's
+    records by the grid (lm_head_topk/lmhead.py:102-103)."""
+    return dev.CU_GRID[0] * dev.CU_GRID[1]
+
+
+def topk_slots(n, slots=None):
+    """Records a top-k call over n output columns writes: one a 32-column tile, or for more tiles than `slots`
+    (default grid_slots(); 0: no limit) one a group of ceil(tiles / slots) consecutive tiles, ranked together."""
+    tiles = -(-n // TILE)
+    slots = grid_slots() if slots is None else slots
+    if slots <= 0 or tiles <= slots:
+        return tiles
+    g = -(-tiles // slots)
+    return -(-tiles // g)
 
 
 def topk_result(device, records, rows, k):

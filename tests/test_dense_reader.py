@@ -183,6 +183,43 @@ def test_topk_records(device):
         same("records against the oracle's", r.cpu().reshape(-1, 2 * rows * kk), torch.from_numpy(words.view(np.int32)))
 
 
+@pytest.mark.parametrize("fp32", [False, True])
+def test_topk_records_grouped(device, fp32):
+    """Blocks wider than the grid's records, their result sized as the reference's callers size it (a block's records
+    are the grid's cores, lm_head_topk/lmhead.py:102-103): two blocks of 16384 columns into one result of
+    2 x grid_slots() records at slot0 = b x grid_slots(). Each launch writes at most its slots (tiles in groups), the
+    other block's slots stay untouched, every record equals the best k of the per-tile records it covers (the same
+    launch with no limit) bit for bit, and bf16 records equal the oracle's ranking of the op's own output."""
+    k, n, rows, kk = 1024, 16384, 3, 8
+    S = linear.grid_slots()
+    x, tx = x_input(device, 4, k, 90)
+    r = linear.topk_result(device, 2 * S, rows, kk)
+    for b in range(2):
+        tw, _ = linear.native_weight(device, matrix(n, k, 91 + b), linear.bfloat8_b)
+        spec = {"r": r, "k": kk, "rows": rows, "slot0": b * S, "base": b * n, "n": n, "write_y": True, "fp32": fp32}
+        p = linear.launch_plan(tx, tw, None, topk=spec)
+        G = p["tiles_per_record"]
+        assert p["records"] == linear.topk_slots(n) <= S and G == -(-(n // 32) // S), p
+        y = host(linear.matmul(tx, tw, None, topk=spec), rows, n)
+        words = r.cpu().reshape(2 * S, -1)
+        if b == 0:
+            assert not words[S:].any(), "block 0 wrote into block 1's slots"
+        one = linear.topk_result(device, n // 32, rows, kk)
+        linear.matmul(tx, tw, None, topk={**spec, "r": one, "slot0": 0, "slots": 0})
+        tv, ti = (t.numpy() for t in linear.topk_records(one, rows, kk, fp32=fp32))
+        gv, gi = (t.numpy() for t in linear.records_host(words[b * S : b * S + p["records"]], rows, kk, fp32=fp32))
+        for g in range(p["records"]):
+            mv, mi = O.global_topk(tv[:, g * G * kk : (g + 1) * G * kk], ti[:, g * G * kk : (g + 1) * G * kk], kk)
+            assert np.array_equal(mv, gv[:, g * kk : (g + 1) * kk]) and np.array_equal(mi, gi[:, g * kk : (g + 1) * kk]), (
+                b, g, mv, gv[:, g * kk : (g + 1) * kk], mi, gi[:, g * kk : (g + 1) * kk])
+        print(f"ok   block {b} (fp32 {fp32}): {p['records']} records of {G} tiles each equal the per-tile records' best "
+              f"{kk}", flush=True)
+        if not fp32:
+            want = O.tile_topk(y.numpy(), rows, kk, n, b * n, width=32 * G)
+            same(f"block {b}: grouped records against the oracle's", words[b * S : b * S + p["records"]],
+                 torch.from_numpy(want.view(np.int32)))
+
+
 def test_block_list_bitwise(device):
     k, m = 1024, 3
     x, tx = x_input(device, m, k, 16)

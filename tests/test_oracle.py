@@ -113,6 +113,30 @@ def test_tile_topk_round_trip():
     assert np.all(np.diff(gv, axis=1) <= 0)
 
 
+def test_tile_topk_groups():
+    """A record of a group of tiles (width 96: three tiles) is the best k of the group's columns by brute force, and
+    the best k of the three tile records it covers (the selection decomposes: highest first, ties to the lower id)."""
+    g = torch.Generator().manual_seed(6)
+    y = torch.randn(2, 200, generator=g).to(torch.bfloat16).float().numpy()
+    y[1, 10] = y[1, 40] = y[1, 70] = 5.0  # a three-way tie across the three tiles of group 0
+    n_valid = 190
+    grouped = O.tile_topk(y, rows=2, k=5, n_valid=n_valid, base=7, width=96)
+    tiles = O.tile_topk(y, rows=2, k=5, n_valid=n_valid, base=7)
+    gv, gi = O.records_decode(grouped, 2, 5)
+    tv, ti = O.records_decode(tiles, 2, 5)
+    assert grouped.shape[0] == 3 and tiles.shape[0] == 7
+    for rec in range(3):
+        for r in range(2):
+            cols = [c for c in range(96 * rec, min(96 * rec + 96, 200)) if c < n_valid]
+            want = sorted(cols, key=lambda c: (-float(y[r, c]), c))[:5]
+            got = gi[r, 5 * rec : 5 * rec + 5]
+            assert [int(i) - 7 for i in got[got >= 0]] == want, (rec, r)
+        lo, hi = 5 * 3 * rec, 5 * min(3 * rec + 3, 7)
+        mv, mi = O.global_topk(tv[:, lo:hi], ti[:, lo:hi], 5)
+        assert np.array_equal(mv, gv[:, 5 * rec : 5 * rec + 5]) and np.array_equal(mi, gi[:, 5 * rec : 5 * rec + 5])
+    assert list(gi[1, :3]) == [7 + 10, 7 + 40, 7 + 70]  # the tie: lower ids first
+
+
 def _eo(fmt, k):
     """Exponent byte of k within a panel, from the layout's statement: groups of 256 k, lane l's four exponents at
     bytes 4 l .. 4 l + 3, lane l making x' for (bfp8) k = 64 j + l, (bfp4) the pair 128 j' + 32 kq + 2 i (+1)."""

@@ -258,7 +258,8 @@ class Workload:
             h = self.heads[i % self.copies]
             if self.m not in h.results:
                 h.logits_topk(self.x, self.m)  # (the result tensor, made once outside any graph)
-            spec = {"r": h.results[self.m], "k": h.k, "rows": self.m, "slot0": 0, "base": 0, "n": h.step, "write_y": False}
+            spec = {"r": h.results[self.m], "k": h.k, "rows": self.m, "slot0": 0, "base": 0, "n": h.step, "write_y": False,
+                    "slots": h.slots}
             L.matmul(self.x, ws[0], None, out=h.y, topk=spec)
         elif o.get("int4"):
             ws[0].w4a16.w4a16_linear(self.x, ws[0].wq, ws[0].ts)

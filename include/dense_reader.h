@@ -105,8 +105,9 @@ typedef struct dr_segment {
  * writes at most max_records records, as the reference's writes at most one a core of its grid (a caller that sizes
  * each block's records by the grid's cores, lm_head_topk/lmhead.py:102-103, stays within them). fp32 0: keys are the
  * reference's bf16 keys of the bf16 output (0 empty) and ids base + column (0xFFFFFFFF empty); fp32 1: keys are the
- * fp32 scores' bits (-inf empty) and ids int32 (-1 empty). Grouped launches (G > 1) need the workspace
- * (dr_workspace_bytes) and at most 1024 = G * k candidates a row and 4096 records. */
+ * fp32 scores' bits (-inf empty) and ids int32 (-1 empty). Grouped launches (G > 1) stage every tile's record in the
+ * workspace (dr_workspace_bytes), rank the groups in a second kernel on the stream, and take at most 1024 = G * k
+ * candidates a row. */
 typedef struct dr_topk {
     void* records;       /* [records_cap][2 * rows * k] uint32, or NULL: no top-k */
     int32_t k;           /* 1 .. 32 */

@@ -108,9 +108,10 @@ struct Args {
     SegDev seg[4];
     uint32_t* rec;
     int tk_k, tk_rows, slot0, n_valid, write_y, tk_fp32, row0;
-    int tk_group;            // tiles a record (> 1: each tile's record is staged in tstage, its group's last merges)
-    uint32_t* gcounters;     // [records] (tk_group > 1): tiles of the group done, reset to 0 by the last
+    int tk_group;            // tiles a record (> 1: each tile's record is staged in tstage, dr_group_k ranks groups)
     uint32_t* tstage;        // [tiles][2 * rows * k] (tk_group > 1): each tile's record
+    uint32_t* rec_out;       // where tile t's record goes: rec_out + t * 2 * rows * k (the host's choice of the record
+                             // slots or the staging: the kernel reads one pointer)
     long long base;
     int chunks, kch, waves;
     int splits, cps, tiles;  // split K: splits workgroups a tile, cps chunks each; tiles of the launch
@@ -674,11 +675,9 @@ __device__ __forceinline__ uint32_t key_f32(float f) {
 //
 // A launch with more tiles than the caller's records writes one record a group of tk_group consecutive tiles (the
 // reference writes one a core, each core's columns ranked together, dense_writer.cpp:185-232). Every tile ranks its
-// own 32 columns into a staging record (device-scope stores), waits for them, and counts itself on its group's
-// counter; the group's last tile reads the group's staged records (device-scope loads) and ranks their candidates by
-// a 64-bit key, the record's key above the id complemented (0 empty), so the order is the tiles' own: highest first,
-// ties to the lower id. It writes the group's record and resets the counter. The device-scope accesses meet at the
-// device's point of coherence as split K's do (the XCDs' L2 caches are not coherent with each other).
+// own 32 columns into a staging record in the workspace; a second kernel on the same stream (dr_group_k, no atomics:
+// the stream orders it after the matmul) ranks each group's candidates by a 64-bit key, the record's key above the id
+// complemented (0 empty), so the order is the tiles' own: highest first, ties to the lower id.
 
 __device__ __forceinline__ unsigned long long cand_key(uint32_t word, uint32_t id, bool fp32) {
     if (id == 0xFFFFFFFFu || (!fp32 && word == 0u)) return 0ull;
@@ -686,51 +685,66 @@ __device__ __forceinline__ unsigned long long cand_key(uint32_t word, uint32_t i
     return ((unsigned long long)ok << 32) | (unsigned long long)(0xFFFFFFFFu - id);
 }
 
-// cand: LDS of at least 2 * tk_group * tk_k words (the launch's dynamic LDS is sized for it)
-__device__ __forceinline__ void topk_group_merge(const Args& a, int t, uint32_t* cand, int mrows) {
-    __shared__ int last;
-    const int G = a.tk_group, K = a.tk_k, R = a.tk_rows;
-    const int grp = t / G, t0 = grp * G, members = min(G, a.tiles - t0);
-    __builtin_amdgcn_s_waitcnt(0);  // this thread's staging stores have reached the point of coherence
-    __syncthreads();
-    if (threadIdx.x == 0)
-        last = __hip_atomic_fetch_add(a.gcounters + grp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-               (uint32_t)(members - 1);
-    __syncthreads();
-    if (!last) return;
+constexpr int GROUP_WAVES = 4;      // dr_group_k: a wavefront a row, rows in turn
+constexpr int GROUP_MAXCAND = 1024;  // candidates a row of a grouped record at most (tiles a record x k)
+
+// one workgroup a record: rows [row0, row1) of the group's staged tile records, each row's best k of the tiles' k.
+// A wavefront takes a row: its lanes load the candidates (word, id) and write each one's 64-bit key to LDS, then each
+// candidate's rank is the count of larger keys (the keys are distinct but for the empty 0).
+__global__ __launch_bounds__(64 * GROUP_WAVES) void dr_group_k(const uint32_t* __restrict__ stage,
+                                                              uint32_t* __restrict__ rec, int tiles, int G, int K, int R,
+                                                              int slot0, int row0, int row1, int fp32) {
+    extern __shared__ unsigned long long keys[];  // [GROUP_WAVES][G * K]
+    const int grp = blockIdx.x, t0 = grp * G, members = min(G, tiles - t0), n = members * K;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const size_t rlen = 2 * (size_t)R * K;
-    const int n = members * K;
-    const bool fp32 = a.tk_fp32 != 0;
-    uint32_t* out = a.rec + (size_t)(a.slot0 + grp) * rlen;
-    for (int m = 0; m < mrows; ++m) {
-        const int r = a.row0 + m;
-        if (r >= R) break;
-        for (int i = threadIdx.x; i < n; i += blockDim.x) {
-            const uint32_t* src = a.tstage + (size_t)(t0 + i / K) * rlen + (size_t)r * K + i % K;
-            cand[i] = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            cand[n + i] = __hip_atomic_load(src + (size_t)R * K, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t* out = rec + (size_t)(slot0 + grp) * rlen;
+    unsigned long long* kw = keys + (size_t)wave * G * K;
+    constexpr int PER = GROUP_MAXCAND / 64;  // candidates a lane at most
+    for (int r = row0 + wave; r < row1; r += GROUP_WAVES) {
+        uint32_t word[PER], id[PER];
+        unsigned long long key[PER];
+        // every load issued before any is used (slots past n read the last candidate again and are dropped)
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            const int i = min(lane + 64 * q, n - 1);
+            const uint32_t* src = stage + (size_t)(t0 + i / K) * rlen + (size_t)r * K + i % K;
+            word[q] = src[0];
+            id[q] = src[(size_t)R * K];
         }
-        __syncthreads();
-        for (int i = threadIdx.x; i < n; i += blockDim.x) {
-            const unsigned long long ci = cand_key(cand[i], cand[n + i], fp32);
-            int rank = 0, nval = 0;
-            for (int j = 0; j < n; ++j) {
-                const unsigned long long cj = cand_key(cand[j], cand[n + j], fp32);
-                rank += cj > ci;
-                nval += cj != 0ull;
-            }
-            if (ci != 0ull && rank < K) {
-                out[(size_t)r * K + rank] = cand[i];
-                out[(size_t)R * K + (size_t)r * K + rank] = cand[n + i];
-            }
-            if (i < K && i >= nval) {
-                out[(size_t)r * K + i] = fp32 ? 0xFF800000u : 0u;
-                out[(size_t)R * K + (size_t)r * K + i] = 0xFFFFFFFFu;
-            }
+        int nval = 0;
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            const int i = lane + 64 * q;
+            key[q] = i < n ? cand_key(word[q], id[q], fp32 != 0) : 0ull;
+            if (i < n) kw[i] = key[q];
+            nval += __popcll(__ballot(key[q] != 0ull));
         }
-        __syncthreads();
+        __builtin_amdgcn_s_waitcnt(0);  // (the wavefront's own LDS writes, read back by its other lanes)
+        __builtin_amdgcn_wave_barrier();
+        int rank[PER];
+#pragma unroll
+        for (int q = 0; q < PER; ++q) rank[q] = 0;
+        const int qn = (n + 63) / 64;  // (the lanes' candidate slots in use, uniform)
+#pragma unroll 8
+        for (int j = 0; j < n; ++j) {
+            const unsigned long long kj = kw[j];
+#pragma unroll
+            for (int q = 0; q < PER; ++q)
+                if (q < qn) rank[q] += kj > key[q];
+        }
+#pragma unroll
+        for (int q = 0; q < PER; ++q)
+            if (key[q] != 0ull && rank[q] < K) {
+                out[(size_t)r * K + rank[q]] = word[q];
+                out[(size_t)R * K + (size_t)r * K + rank[q]] = id[q];
+            }
+        for (int q = nval + lane; q < K; q += 64) {
+            out[(size_t)r * K + q] = fp32 ? 0xFF800000u : 0u;
+            out[(size_t)R * K + (size_t)r * K + q] = 0xFFFFFFFFu;
+        }
+        __builtin_amdgcn_wave_barrier();  // (this row's keys read before the next row's overwrite them)
     }
-    if (threadIdx.x == 0) __hip_atomic_store(a.gcounters + grp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---- expert gather: ids, the union of the rows' ids ----------------------------------------------------------------
@@ -899,29 +913,27 @@ __device__ __forceinline__ void epilogue(const Args& a, const SegDev& sg, int t,
     }
     if (!topk) return;
     __syncthreads();
-    const bool grouped = a.tk_group > 1;
     // one wavefront ranks each row's 32 keys: the best k, highest first, ties to the lower column. The record goes to
-    // its slot, or (grouped) to the tile's staging slot, with device-scope stores that the group's last tile reads.
+    // its slot, or with grouped records to the tile's staging record (dr_group_k ranks the groups afterwards).
     if (wave == 0) {
         const int K = a.tk_k, R = a.tk_rows;
         const size_t rlen = 2 * (size_t)R * K;
-        uint32_t* rec = grouped ? a.tstage + (size_t)t * rlen : a.rec + (size_t)(a.slot0 + t) * rlen;
-        auto put = [grouped](uint32_t* p, uint32_t v) {
-            if (grouped)
-                __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            else
-                *p = v;
-        };
+        uint32_t* rec = a.rec_out + (size_t)t * rlen;
+        auto put = [](uint32_t* p, uint32_t v) { *p = v; };
         for (int m = 0; m < mrows; ++m) {
             const int r = a.row0 + m;
             if (r >= R) break;
             const int c = lane & 31;
             const uint32_t key = tkey[m][c];
+            // rank: the columns ahead of c, by key then the lower column first (one 64-bit compare a column: the
+            // key above the column complemented)
+            const unsigned long long me = ((unsigned long long)key << 32) | (uint32_t)(TILE - 1 - c);
             int rank = 0, nval = 0;
+#pragma unroll 4
             for (int j = 0; j < TILE; ++j) {
                 const uint32_t kj = tkey[m][j];
                 nval += kj != 0u;
-                rank += (kj > key) || (kj == key && j < c);
+                rank += (((unsigned long long)kj << 32) | (uint32_t)(TILE - 1 - j)) > me;
             }
             if (lane < 32 && key != 0u && rank < K) {
                 const float val = tval[m][c];
@@ -934,7 +946,6 @@ __device__ __forceinline__ void epilogue(const Args& a, const SegDev& sg, int t,
             }
         }
     }
-    if (grouped) topk_group_merge(a, t, reinterpret_cast<uint32_t*>(const_cast<float*>(part)), mrows);
 }
 
 // the gate/up modes' epilogue: thread (m, col) of the tile adds the bias, applies the GLU and the row's routing weight
@@ -1009,8 +1020,6 @@ __device__ __forceinline__ void moe_zero(const MoeArgs& a, int t, int unit) {
 #define DR_SPLIT_MAXTILES 16384
 #endif
 constexpr int SPLIT_MAXTILES = DR_SPLIT_MAXTILES;  // counters in the workspace: tiles of a split launch at most
-constexpr int GROUP_MAXRECORDS = 4096;  // record-group counters in the workspace: records of a grouped launch at most
-constexpr int GROUP_MAXCAND = 1024;     // candidates a row of a grouped record at most (tiles a record x k)
 
 __device__ __forceinline__ void st_dev(float* p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -2025,11 +2034,9 @@ int rows_per_pass(int m) {
     return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
 }
 
-// dynamic LDS of a dense launch: the partial sums, or a grouped record's candidates (2 * tiles a record * k words)
+// dynamic LDS of a dense launch: the partial sums
 size_t dense_lds(const Args& a, int pw, int rows) {
-    const size_t sums = (size_t)max(a.waves, a.splits) * pw * rows * 16 * sizeof(float);
-    const size_t cand = a.rec != nullptr && a.tk_group > 1 ? (size_t)2 * a.tk_group * a.tk_k * sizeof(uint32_t) : 0;
-    return max(sums, cand);
+    return (size_t)max(a.waves, a.splits) * pw * rows * 16 * sizeof(float);
 }
 
 template <int MR, int PW>
@@ -2310,10 +2317,11 @@ int prepare(const dr_launch* L, Args& a, int& pw, int& tiles, int& mr, bool gath
         if (T.max_records > 0 && tiles > T.max_records) a.tk_group = (tiles + T.max_records - 1) / T.max_records;
         const int records = (tiles + a.tk_group - 1) / a.tk_group;
         if ((int64_t)T.slot0 + records > T.records_cap) return DR_EINVAL;
-        if (a.tk_group > 1 && (a.tk_group * T.k > GROUP_MAXCAND || records > GROUP_MAXRECORDS)) return DR_ERANGE;
+        if (a.tk_group > 1 && a.tk_group * T.k > GROUP_MAXCAND) return DR_ERANGE;
         a.tk_k = T.k;
         a.tk_rows = T.rows;
         a.slot0 = T.slot0;
+        a.rec_out = a.rec + (size_t)T.slot0 * 2 * T.rows * T.k;  // (grouped: the staging, once the workspace is bound)
         a.n_valid = T.n_valid;
         a.base = T.base;
         a.write_y = T.write_y != 0;
@@ -2345,10 +2353,9 @@ int prepare(const dr_launch* L, Args& a, int& pw, int& tiles, int& mr, bool gath
     return DR_OK;
 }
 
-// The workspace: SPLIT_MAXTILES split-K counters and GROUP_MAXRECORDS record-group counters at fixed places (so that
-// launches of any shape can share one), then split K's column sums (every workgroup's), then the grouped records'
-// staging (every tile's record).
-constexpr int64_t WS_COUNTERS = ((int64_t)SPLIT_MAXTILES + GROUP_MAXRECORDS) * 4;
+// The workspace: SPLIT_MAXTILES split-K counters at a fixed place (so that launches of any shape can share one), then
+// split K's column sums (every workgroup's), then the grouped records' staging (every tile's record).
+constexpr int64_t WS_COUNTERS = (int64_t)SPLIT_MAXTILES * 4;
 
 int64_t split_sums_bytes(const Args& a, int pw, int mr) {
     return a.splits > 1 ? (int64_t)a.tiles * a.splits * pw * mr * 16 * 4 : 0;
@@ -2363,9 +2370,9 @@ int64_t workspace_bytes(const Args& a, int pw, int mr) {
 void bind_split(Args& a, void* workspace, int pw, int mr) {
     uint8_t* w = reinterpret_cast<uint8_t*>(workspace);
     a.counters = reinterpret_cast<uint32_t*>(w);
-    a.gcounters = reinterpret_cast<uint32_t*>(w + (int64_t)SPLIT_MAXTILES * 4);
     a.wpart = reinterpret_cast<float*>(w + WS_COUNTERS);
     a.tstage = reinterpret_cast<uint32_t*>(w + WS_COUNTERS + split_sums_bytes(a, pw, mr));
+    if (a.rec != nullptr && a.tk_group > 1) a.rec_out = a.tstage;
 }
 
 // dr_matmul's launches: one pass of up to mr rows each (the passes a top-k launch needs, not y, skipped)
@@ -2379,7 +2386,14 @@ int run_passes(const dr_launch* L, const Args& a, int tiles, int mr, int pw, hip
         if (a.res) p.res = a.res + (size_t)r0 * a.ldr;
         p.row0 = r0;
         if (a.rec != nullptr && r0 >= a.tk_rows && !a.write_y) continue;
-        const hipError_t e = launch_rows(p, mr, pw, tiles * a.splits, st);
+        hipError_t e = launch_rows(p, mr, pw, tiles * a.splits, st);
+        if (e == hipSuccess && a.rec != nullptr && a.tk_group > 1 && r0 < a.tk_rows) {
+            const int records = (tiles + a.tk_group - 1) / a.tk_group;
+            const size_t lds = (size_t)GROUP_WAVES * a.tk_group * a.tk_k * sizeof(unsigned long long);
+            hipLaunchKernelGGL(dr_group_k, dim3(records), dim3(64 * GROUP_WAVES), lds, st, a.tstage, a.rec, tiles,
+                               a.tk_group, a.tk_k, a.tk_rows, a.slot0, r0, min(r0 + p.m, a.tk_rows), a.tk_fp32);
+            e = hipGetLastError();
+        }
         if (e != hipSuccess) return DR_EHIP;
     }
     return DR_OK;
@@ -2390,9 +2404,8 @@ int run_passes(const dr_launch* L, const Args& a, int tiles, int mr, int pw, hip
 // A file-scope device array, one copy on every GPU the library runs on, held until the process ends. Host code never
 // uses its name as an address (on the host it is only a stand-in for the symbol): each device's address comes from
 // hipGetSymbolAddress, once per device with that device current, and that address is what kernels and fills get.
-// It serves as dr_matmul's workspace: the counters (split K's and the record groups') must start at zero (a fill kernel
-// clears them on a device's first call; every launch leaves them at zero), the partial sums and staging need no
-// clearing.
+// It serves as dr_matmul's workspace: the split-K counters must start at zero (a fill kernel clears them on a device's
+// first call; every launch leaves them at zero), the partial sums and the records' staging need no clearing.
 static __device__ __align__(256) uint8_t scratch[DR_SCRATCH_BYTES];
 
 __global__ __launch_bounds__(256) void dr_zero_k(uint32_t* __restrict__ p, int n) {
@@ -2412,7 +2425,7 @@ void* scratch_for_current_device(hipStream_t st) {
     if (scratch_addr[d] == nullptr) {
         void* ptr = nullptr;
         if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) return nullptr;
-        constexpr int n = (int)(WS_COUNTERS / 4);  // the counters: split K's, then the record groups
+        constexpr int n = (int)(WS_COUNTERS / 4);  // the split-K counters
         hipLaunchKernelGGL(dr_zero_k, dim3((n + 255) / 256), dim3(256), 0, st, reinterpret_cast<uint32_t*>(ptr), n);
         if (hipGetLastError() != hipSuccess) return nullptr;
         scratch_addr[d] = ptr;

@@ -203,3 +203,38 @@ def test_records_pick(device):
     assert int(ids_out.cpu()[0]) == int(tmap[best[0]])
     for h in (plain, picked, mapped):
         h.deallocate()
+
+
+def test_wide_blocks(device):
+    """The reference's head sizing with blocks wider than the grid's records (lm_head_topk/lmhead.py:102-103: a
+    block's records are the grid's cores, block b's from slot b * cores): two blocks of 16384 columns (512 tiles)
+    into 2 x grid_slots() records. Every launch stays within its block's slots (tile pairs share a record), and the
+    device pick over those records gives the oracle's pick of them and the bf16 head's tokens."""
+    vocab, dim, chunks, k, rows = 32768, 512, 2, 8, 3
+    step, S = vocab // chunks, linear.grid_slots()
+    g = torch.Generator().manual_seed(21)
+    w = (torch.randn(vocab, dim, generator=g) * 0.05).to(torch.bfloat16)
+    x = torch.randn(rows, dim, generator=g).to(torch.bfloat16)
+    tx = x.reshape(1, 1, rows, dim).to(device.torch)
+    assert step // 32 > S, (step, S)
+    r = linear.topk_result(device, chunks * S, rows, k)
+    y = torch.empty(1, 1, rows, step, dtype=torch.bfloat16, device=device.torch)
+    for b in range(chunks):
+        tw, _ = linear.native_weight(device, w[b * step : (b + 1) * step].float(), linear.bfloat8_b)
+        spec = {"r": r, "k": k, "rows": rows, "slot0": b * S, "base": b * step, "n": step, "write_y": False}
+        linear.matmul(tx, tw, None, topk=spec, out=y)
+    vals, ids = linear.topk_records(r, rows, k)
+    ids = ids.reshape(rows, chunks, -1)
+    for b in range(chunks):
+        ok = ids[:, b] >= 0
+        assert bool(((ids[:, b] // step == b) | ~ok).all()), f"block {b}'s slots hold another block's ids"
+        assert bool(ok.all()), f"block {b}: every slot filled (each record spans 64 columns)"
+    rows_t = head_pick.head_rows(device, w)
+    tok, _, _ = head_pick.tokens(head_pick.pick(r, tx, rows_t, rows, k, top=16), rows)
+    words = r.reshape(r.shape[-2], -1).cpu().numpy()
+    want, _, _ = O.pick_from_records(words, rows, k, 16, x, w, "bf16", vocab)
+    z = O.head_logits(x, w).numpy()
+    same_tokens("wide blocks sized by the grid: device pick against the oracle's pick of the records", tok.numpy(),
+                want, z)
+    true = O.pick_token(z, np.broadcast_to(np.arange(vocab), z.shape), vocab)
+    same_tokens("wide blocks sized by the grid: device pick against the bf16 head", tok.numpy(), true, z)

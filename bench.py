@@ -2,6 +2,8 @@
 
   python bench.py [--steps K] [--warmup W] [--config ns|c1|c2|c3|c4|c5|int4|moe|lm] [--no-cpu] [--cpu-seconds S]
   python bench.py --copy-probe      (a plain 256 MiB copy kernel: the byte counters' calibration under rocprofv3)
+  python bench.py --read-probe BYTES  (the read ceiling: dr_stream_read of BYTES, timed as a config is)
+  --no-eager: skip the eager timing loop (rocprofv3 traces then hold the graph-replayed launches but the warm-up's)
 
 Default workload: the north-star decode matmul, bfloat8_b M=1, x [1, 4096] bf16 @ W [4096 in, 14336 out] (W ~
 N(0, 0.02)), no fused stage, bf16 output. A step is one call of the op (c5: the matmul with top-k records, then the
@@ -100,6 +102,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--copy-probe", action="store_true")
+    ap.add_argument("--read-probe", type=int, default=0, metavar="BYTES")
+    ap.add_argument("--no-eager", action="store_true")
     ap.add_argument("--kblock", action="store_true",
                     help="config moe: the experts packed with their shared exponents along K (moe8.pack(kblock=True))")
     return ap.parse_args()
@@ -116,6 +120,52 @@ def copy_probe():
         torch.neg(src, out=dst)
     torch.cuda.synchronize()
     print(json.dumps({"copy_probe": "torch.neg float32", "read_bytes": 4 * n, "write_bytes": 4 * n}), flush=True)
+
+
+def read_probe(torch, nbytes, steps, warmup):
+    """The read ceiling: `steps` launches of dr_stream_read over nbytes each, rotating over enough buffers (>= 512 MB)
+    that the Infinity Cache cannot serve them, captured in a HIP graph and timed as a config's steps are."""
+    from dense_reader import _lib
+
+    lib = _lib.lib()
+    nbytes = nbytes // 16 * 16
+    copies = max(2, math.ceil(MALL_BYTES / nbytes) + 1)
+    bufs = [torch.ones(nbytes, dtype=torch.uint8, device="cuda") for _ in range(copies)]
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+
+    def step(i):
+        st = torch.cuda.current_stream()
+        _lib.check(lib.dr_stream_read(bufs[i % copies].data_ptr(), nbytes, sink.data_ptr(), st.cuda_stream),
+                   "dr_stream_read")
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    ms = timed_graph(torch, step, steps)
+    us = ms * 1e3 / steps
+    print(json.dumps({"read_probe": "dr_stream_read", "bytes": nbytes, "steps": steps, "buffers_rotated": copies,
+                      "us_per_launch": round(us, 3), "GB/s": round(nbytes / (us * 1e-6) / 1e9, 2),
+                      "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}), flush=True)
+
+
+MFMA_TABLE = ROOT / "profiles" / "mfma_l2.md"
+MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
+
+
+def mfma_row(name):
+    """The counter figures of config `name` from profiles/mfma_l2.md (a row `| name | kernel | rows | TFLOP/s | % of
+    peak | busy % | L1 -> L2 MB | x weight bytes | L2 hit % |`), or None."""
+    if not MFMA_TABLE.exists():
+        return None
+    for line in MFMA_TABLE.read_text().splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) == 9 and cells[0] == name:
+            try:
+                return {"counter_tflops": float(cells[3]), "counter_pct_of_peak": float(cells[4]),
+                        "busy_pct": float(cells[5]), "l1_to_l2_read_mb": float(cells[6]), "l2_hit_pct": float(cells[8])}
+            except ValueError:
+                return None
+    return None
 
 
 def traffic_row(name):
@@ -330,6 +380,9 @@ def main():
     if a.copy_probe:
         copy_probe()
         return
+    if a.read_probe:
+        read_probe(torch, a.read_probe, a.steps, a.warmup)
+        return
 
     from dense_reader import linear
 
@@ -343,7 +396,7 @@ def main():
 
     # eager: each call bracketed by events on its stream (host launch cost included)
     st = torch.cuda.current_stream()
-    nev = min(a.steps, 100)
+    nev = 0 if a.no_eager else min(a.steps, 100)
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(nev)]
     for i in range(nev):
         ev[i][0].record(st)
@@ -362,6 +415,15 @@ def main():
     achieved = kbytes / (launch_us * 1e-6) / 1e9
 
     cpu = None if a.no_cpu else cpu_baseline(wl, a.cpu_seconds)
+    # the MFMA configs (more than 2 rows): the matrix cores' rate over the launch (rows padded to the 16- or 32-row
+    # MFMA tile), live, and the counter figures of profiles/mfma_l2.md
+    mfma = None
+    if wl.m > 2 and not wl.o.get("moe") and not wl.o.get("int4"):
+        mpad = 16 if wl.m <= 16 else 32
+        nsum = wl.spec[0][0] * 2 if wl.o.get("glu2") else sum(n for n, _, _ in wl.spec)
+        tflops = 2 * mpad * wl.k * nsum / (launch_us * 1e-6) / 1e12
+        mfma = {"rows_in_tiles": mpad, "tflops": round(tflops, 2), "peak_tflops": MFMA_PEAK_TFLOPS,
+                "frac": round(tflops / MFMA_PEAK_TFLOPS, 4), **(mfma_row(a.config) or {})}
     fmts = sorted({f for _, f, _ in wl.spec})
     line = {
         "metric": METRIC,
@@ -392,7 +454,7 @@ def main():
                if wl.o.get("moe") else {}),
             "timing": "HIP graph of the timed steps, replayed; events on the replay stream",
         },
-        "eager_us_per_call": {"median": round(eager[len(eager) // 2], 3), "min": round(eager[0], 3)},
+        "eager_us_per_call": {"median": round(eager[len(eager) // 2], 3), "min": round(eager[0], 3)} if eager else None,
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 2),
@@ -402,6 +464,7 @@ def main():
             "traffic": traffic_row(a.config),
             "launch_us": round(launch_us, 3),
             "algorithmic_bytes": kbytes,
+            "mfma": mfma,
         },
         "cpu_baseline": cpu,
     }

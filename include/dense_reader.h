@@ -196,6 +196,11 @@ typedef struct dr_launch_info {
 } dr_launch_info;
 int dr_launch_plan(const dr_launch* launch, dr_launch_info* info);
 
+/* A plain streaming read of `bytes` (a multiple of 16, 16-byte aligned) at p with every CU: the read ceiling the
+ * matmul's weight bandwidth is measured against (bench.py --read-probe). No counterpart in the reference (a
+ * measurement aid); nothing is written but, never in practice, one word of sink. */
+int dr_stream_read(const void* p, int64_t bytes, uint32_t* sink, void* stream);
+
 const char* dr_status_string(int status);
 int dr_version(void);
 

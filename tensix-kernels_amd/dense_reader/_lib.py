@@ -31,6 +31,7 @@ SYMBOLS = (
     "dr_topk_merge_workspace_bytes",
     "dr_plan",
     "dr_launch_plan",
+    "dr_stream_read",
     "dr_status_string",
     "dr_version",
     "dr_head_pick",
@@ -206,6 +207,8 @@ def lib():
         L.dr_plan.argtypes = [c_int, c_int, ctypes.POINTER(c_int32), ctypes.POINTER(c_int32), ctypes.POINTER(c_int32)]
         L.dr_launch_plan.restype = c_int
         L.dr_launch_plan.argtypes = [ctypes.POINTER(Launch), ctypes.POINTER(LaunchInfo)]
+        L.dr_stream_read.restype = c_int
+        L.dr_stream_read.argtypes = [c_void_p, c_int64, c_void_p, c_void_p]
         L.dr_status_string.restype = ctypes.c_char_p
         L.dr_status_string.argtypes = [c_int]
         L.dr_version.restype = c_int

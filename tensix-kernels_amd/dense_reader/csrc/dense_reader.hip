@@ -1963,6 +1963,29 @@ __global__ __launch_bounds__(SEL_T) void dr_merge_k(SelArgs A, int fp32, float* 
     ids[(size_t)r * A.keep + lane] = id;
 }
 
+// ---- the read ceiling (measurement) --------------------------------------------------------------------------------
+//
+// A plain streaming read with every CU, the ceiling the matmul's weight bandwidth is compared against: one workgroup
+// of READ_T threads a READ_T * READ_U * 16-byte slice, each thread's READ_U non-temporal 16-byte loads all issued
+// before any is used (of the shapes tried on MI355X -- slices of 32 KB to 128 KB a workgroup, or a persistent grid of
+// one or two workgroups a CU looping over the buffer -- the 32 KB slices read fastest). The loaded words are folded and
+// compared with a value they never take, so the loads stay and nothing is written.
+constexpr int READ_T = 512, READ_U = 4;
+
+__global__ __launch_bounds__(READ_T) void dr_read_k(const u32x4_t* __restrict__ p, long long n16, uint32_t* sink) {
+    const long long base = (long long)blockIdx.x * READ_T * READ_U + threadIdx.x;
+    u32x4_t v[READ_U];
+#pragma unroll
+    for (int u = 0; u < READ_U; ++u) {
+        const long long i = min(base + (long long)u * READ_T, n16 - 1);
+        v[u] = __builtin_nontemporal_load(p + i);
+    }
+    uint32_t acc = 0;
+#pragma unroll
+    for (int u = 0; u < READ_U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    if (acc == 0x9E3779B9u && threadIdx.x == 0) sink[0] = acc;
+}
+
 inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 int hip_status(hipError_t e) { return e == hipSuccess ? DR_OK : DR_EHIP; }
@@ -2463,6 +2486,15 @@ int dr_matmul(const dr_launch* L) {
 }
 
 int64_t dr_scratch_bytes(void) { return DR_SCRATCH_BYTES; }
+
+int dr_stream_read(const void* p, int64_t bytes, uint32_t* sink, void* stream) {
+    if (p == nullptr || sink == nullptr || bytes < 16 || bytes % 16 || (reinterpret_cast<uintptr_t>(p) & 15)) return DR_EINVAL;
+    const long long n16 = bytes / 16;
+    const long long per = (long long)READ_T * READ_U;
+    hipLaunchKernelGGL(dr_read_k, dim3((unsigned)((n16 + per - 1) / per)), dim3(READ_T), 0, S(stream),
+                       reinterpret_cast<const u32x4_t*>(p), n16, sink);
+    return hip_status(hipGetLastError());
+}
 
 int dr_matmul_noalloc(const dr_launch* L) {
     Args a{};

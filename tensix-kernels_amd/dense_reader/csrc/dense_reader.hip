@@ -1333,6 +1333,59 @@ __device__ __forceinline__ void x_kmask(uint4& v, const Args& a, int k) {
     if (k >= a.k) v = make_uint4(0u, 0u, 0u, 0u);
 }
 
+// 32-row launches stage x through LDS, each wavefront in 8 KB of its own. x_row8's loads give a lane its operand
+// directly, but one load then spans 16 rows, 64 bytes of a 128-byte line in each, and at 32 rows x is most of what a
+// workgroup reads. XStage::stage copies the 32 rows over k0 .. k0 + 8 NCH - 1 to LDS with buffer loads straight to
+// LDS (buffer_load_dwordx4 ... lds: lane l's 16 bytes land at slot 64 i + l of load i), each load 64 / NCH whole rows
+// of that range, whole lines; x_lds then reads the operands. Row r's 8-value chunk c sits at slot NCH r + (c ^ s(r)),
+// s(r) = r & 15 with 16 chunks a row, (r >> 1) & 7 with 8: the 16 rows of one operand read hit 16 different bank
+// groups. A lane's offset into x is fixed for the whole K loop but for the step's k and the load's rows, one add a
+// load: for load i its row is 64 i / NCH + l / NCH and its chunk (l % NCH) ^ s(row), which is the lane's chunk of
+// load 0 with 4 (i & 3) (16 chunks) or 4 (i & 1) (8 chunks) xored in. The buffer ends with x's last row, so rows past
+// x and the columns past the last row's end read as zeros (the rows only reach output rows that are never written;
+// the columns past K are zeroed by x_kmask as in x_row8).
+constexpr int XS_BYTES = 8192;  // a wavefront's staging: 32 rows x 128 k of bf16
+template <int NCH>
+__device__ __forceinline__ int x_swz(int row) {
+    static_assert(NCH == 8 || NCH == 16, "x_swz: 8 or 16 chunks a row");
+    return NCH == 16 ? (row & 15) : ((row >> 1) & 7);
+}
+template <int NCH>
+struct XStage {
+    static_assert(NCH * 16 * 32 <= XS_BYTES, "XStage: the staging holds 32 rows of 8 NCH values");
+    static constexpr int RPI = 64 / NCH;  // rows a load covers
+    __amdgpu_buffer_rsrc_t r;
+    uint32_t off[4];  // the lane's byte offset for loads i with (i & 3) == j (16 chunks) or (i & 1) == j (8)
+    uint32_t ldx2;
+    __device__ __forceinline__ XStage(const Args& a, int lane) {
+        ldx2 = 2u * (uint32_t)a.ldx;
+        r = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)(ldx2 * (uint32_t)a.m), 0x00020000);
+        const int l = (int)opaque((uint32_t)lane);  // (made per chunk, not held across the kernel's chunk loop)
+        const int row = l / NCH, c0 = (l % NCH) ^ x_swz<NCH>(row);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) off[j] = (uint32_t)row * ldx2 + 16u * (uint32_t)(c0 ^ (4 * j));
+    }
+    __device__ __forceinline__ void stage(int k0, uint4* xs) const {
+        // the wavefront's reads of the previous staging have returned before these loads may land on it (s_waitcnt
+        // lgkmcnt(0): the loads write LDS when they return, outside the order of the wavefront's own LDS instructions)
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        // (opaque: the offsets of all the loads, hoisted out of the K loop, would hold 8 registers)
+        uint32_t o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = opaque(off[j]) + 2u * (uint32_t)k0;
+#pragma unroll
+        for (int i = 0; i < 32 / RPI; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(xs + 64 * i), 16,
+                                                     o[NCH == 16 ? (i & 3) : (i & 1)] + (uint32_t)(RPI * i) * ldx2, 0,
+                                                     0, 0);
+    }
+};
+// the operand x_row8(a, row, k0 + 8 c) would give, from the staging of k0 (row < 32)
+template <int NCH>
+__device__ __forceinline__ uint4 x_lds(const uint4* xs, int row, int c) {
+    return xs[NCH * row + (c ^ x_swz<NCH>(row))];
+}
+
 __device__ __forceinline__ f32x4 mfma(uint4 a, uint4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
@@ -1575,8 +1628,172 @@ __device__ __forceinline__ void mgroup_bf16(const Args& a, const uint8_t* const*
             for (int tt = 0; tt < MT; ++tt) acc[q][tt] = mfma(A[u][tt], c[u][q], acc[q][tt]);
 }
 
+// ---- 32 rows: a wavefront's chunk in steps of 128 k, software-pipelined ---------------------------------------------
+//
+// Step s + 1's x is staged and its codes loaded while step s is decoded and multiplied, so one step's loads are in
+// flight during the compute of the step before (without that, every wavefront of a workgroup waits for its loads and
+// then computes, together, and the CU idles through half of each). Step s's x operands are read from the staging into
+// registers before step s + 1's loads are issued into the same 8 KB, which keeps a workgroup's LDS small enough for
+// two workgroups a CU. The sums are those of mgroup_* in the same order, so the results are the same bit for bit.
+
+// x operands of one step of 8 NCH k: A[j][tt] = rows 16 tt + r, the 8 values of chunk chunk(j, kq) (zeroed past K)
+template <int NCH, int NJ, typename F>
+__device__ __forceinline__ void xl_operands(const Args& a, const uint4* xb, int k, int lane, uint4 (&A)[NJ][2], F chunk) {
+    const int r = lane & 15, kq = lane >> 4;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) A[j][tt] = x_lds<NCH>(xb, 16 * tt + r, chunk(j, kq));
+    if (a.k != a.k_pad && k + 8 * NCH > a.k) {  // (a ragged K's last step only)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) x_kmask(A[j][tt], a, k + 8 * chunk(j, kq));
+    }
+}
+
+// bfloat8_b: a step is blocks k / 64 and k / 64 + 1 (k0, k1 multiples of 256: a group is two steps); MFMA (b, h) takes
+// k = 64 b + 16 kq + 8 h + j of the step
+template <int PW>
+__device__ __forceinline__ void xl_chunk_bfp8(const Args& a, const uint8_t* const* cb, const uint8_t* const* eb, int k0,
+                                              int k1, int lane, f32x4 (&acc)[PW][2], uint4* xs) {
+    const int ns = (k1 - k0) >> 7;
+    const XStage<16> xst(a, lane);
+    uint4 cn[2][PW];
+    uint32_t en[PW], e[PW];
+    auto issue = [&](int s) {
+        const int k = k0 + 128 * s;
+        xst.stage(k, xs);
+        if (!(s & 1)) {
+#pragma unroll
+            for (int q = 0; q < PW; ++q) en[q] = ld_stream4(eb[q] + (uint32_t)(k + 4 * lane));  // (group k / 256)
+        }
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int q = 0; q < PW; ++q) cn[b][q] = ld_stream16(cb[q] + (uint32_t)(((k >> 6) + b) * 1024 + lane * 16));
+    };
+    issue(0);
+    for (int s = 0; s < ns; ++s) {
+        const int k = k0 + 128 * s;
+        uint4 c[2][PW];
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int q = 0; q < PW; ++q) c[b][q] = cn[b][q];
+        if (!(s & 1)) {
+#pragma unroll
+            for (int q = 0; q < PW; ++q) e[q] = en[q];
+        }
+        uint4 A[4][2];  // [2 b + h][tt]
+        xl_operands<16, 4>(a, xs, k, lane, A, [](int j, int kq) { return 8 * (j >> 1) + 2 * kq + (j & 1); });
+        if (s + 1 < ns) issue(s + 1);
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int q = 0; q < PW; ++q) {
+                const float sc = __builtin_ldexpf(1.f, (int)((e[q] >> (8 * (2 * (s & 1) + b))) & 0xFFu) - 133);
+                const uint4 B0 = b_bfp8<0>(c[b][q], sc);
+                const uint4 B1 = b_bfp8<1>(c[b][q], sc);
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+                    acc[q][tt] = mfma(A[2 * b][tt], B0, acc[q][tt]);
+                    acc[q][tt] = mfma(A[2 * b + 1][tt], B1, acc[q][tt]);
+                }
+            }
+    }
+}
+
+// bfloat4_b: a step is block k / 128; MFMA D takes k = 32 kq + 8 D + j of the step
+template <int PW>
+__device__ __forceinline__ void xl_chunk_bfp4(const Args& a, const uint8_t* const* cb, const uint8_t* const* eb, int k0,
+                                              int k1, int lane, f32x4 (&acc)[PW][2], uint4* xs) {
+    const int ns = (k1 - k0) >> 7;
+    const XStage<16> xst(a, lane);
+    uint4 cn[PW];
+    uint32_t en[PW], e[PW];
+    auto issue = [&](int s) {
+        const int k = k0 + 128 * s;
+        xst.stage(k, xs);
+        if (!(s & 1)) {
+#pragma unroll
+            for (int q = 0; q < PW; ++q) en[q] = ld_stream4(eb[q] + (uint32_t)(k + 4 * lane));
+        }
+#pragma unroll
+        for (int q = 0; q < PW; ++q) cn[q] = ld_stream16(cb[q] + (uint32_t)(real_block(k >> 7, a.k) * 1024 + lane * 16));
+    };
+    issue(0);
+    for (int s = 0; s < ns; ++s) {
+        const int k = k0 + 128 * s;
+        uint4 c[PW];
+#pragma unroll
+        for (int q = 0; q < PW; ++q) c[q] = cn[q];
+        if (!(s & 1)) {
+#pragma unroll
+            for (int q = 0; q < PW; ++q) e[q] = en[q];
+        }
+        uint4 A[4][2];  // [D][tt]
+        xl_operands<16, 4>(a, xs, k, lane, A, [](int j, int kq) { return 4 * kq + j; });
+        if (s + 1 < ns) issue(s + 1);
+#pragma unroll
+        for (int q = 0; q < PW; ++q) {
+            const uint32_t ep = e[q] >> (16 * (s & 1));
+            const float s0 = __builtin_ldexpf(1.f, (int)(ep & 0xFFu) - 133);
+            const float s1 = __builtin_ldexpf(1.f, (int)((ep >> 8) & 0xFFu) - 133);
+            const uint4 B0 = b_bfp4<0>(c[q].x, s0, s1);
+            const uint4 B1 = b_bfp4<1>(c[q].y, s0, s1);
+            const uint4 B2 = b_bfp4<2>(c[q].z, s0, s1);
+            const uint4 B3 = b_bfp4<3>(c[q].w, s0, s1);
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                acc[q][tt] = mfma(A[0][tt], B0, acc[q][tt]);
+                acc[q][tt] = mfma(A[1][tt], B1, acc[q][tt]);
+                acc[q][tt] = mfma(A[2][tt], B2, acc[q][tt]);
+                acc[q][tt] = mfma(A[3][tt], B3, acc[q][tt]);
+            }
+        }
+    }
+}
+
+// bf16: a step is 64 k, blocks k / 32 and k / 32 + 1 (its 4 KB of codes a panel pair: half the bfloat8_b step's
+// registers for a 128-k step's 8 KB); MFMA u takes k = 32 u + 8 kq + j of the step
+template <int PW>
+__device__ __forceinline__ void xl_chunk_bf16(const Args& a, const uint8_t* const* cb, int k0, int k1, int lane,
+                                              f32x4 (&acc)[PW][2], uint4* xs) {
+    const int ns = (k1 - k0) >> 6;
+    const XStage<8> xst(a, lane);
+    uint4 cn[2][PW];
+    auto issue = [&](int s) {
+        const int k = k0 + 64 * s;
+        xst.stage(k, xs);
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int q = 0; q < PW; ++q) cn[u][q] = ld_stream16(cb[q] + (uint32_t)(((k >> 5) + u) * 1024 + lane * 16));
+    };
+    issue(0);
+    for (int s = 0; s < ns; ++s) {
+        const int k = k0 + 64 * s;
+        uint4 c[2][PW];
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int q = 0; q < PW; ++q) c[u][q] = cn[u][q];
+        uint4 A[2][2];  // [u][tt]
+        xl_operands<8, 2>(a, xs, k, lane, A, [](int j, int kq) { return 4 * j + kq; });
+        if (s + 1 < ns) issue(s + 1);
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int q = 0; q < PW; ++q)
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) acc[q][tt] = mfma(A[u][tt], c[u][q], acc[q][tt]);
+    }
+}
+
 template <int MT, int PW, int FMT, bool ONE>
-__global__ __launch_bounds__(512) void dr_mfma(const Args a) {
+__global__ __launch_bounds__(512, MT == 2 ? 4 : 1) void dr_mfma(const Args a) {  // (32 rows: 4 wavefronts a SIMD, so
+                                                                                 // two workgroups a CU)
     constexpr int ROWS = 16 * MT;
     extern __shared__ float part[];  // [W][PW][ROWS][16]
     __shared__ float tval[ROWS][TILE];
@@ -1598,10 +1815,17 @@ __global__ __launch_bounds__(512) void dr_mfma(const Args a) {
     for (int q = 0; q < PW; ++q)
 #pragma unroll
         for (int tt = 0; tt < MT; ++tt) acc[q][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // 32 rows: x through the wavefront's LDS staging, which the partial sums overwrite after the K loop
+    constexpr bool XL = MT == 2;
+    uint4* xs = reinterpret_cast<uint4*>(part) + wave * (XS_BYTES / 16);
     const int ch1 = min((split + 1) * a.cps, a.chunks);
     for (int ch = split * a.cps + wave; ch < ch1; ch += a.waves) {
         const int k0 = ch * a.kch, k1 = min(k0 + a.kch, a.k_pad);
-        if (fmt == DR_BFP8) {
+        if constexpr (XL) {
+            if (fmt == DR_BFP8) xl_chunk_bfp8<PW>(a, cb, eb, k0, k1, lane, acc, xs);
+            else if (fmt == DR_BFP4) xl_chunk_bfp4<PW>(a, cb, eb, k0, k1, lane, acc, xs);
+            else xl_chunk_bf16<PW>(a, cb, k0, k1, lane, acc, xs);
+        } else if (fmt == DR_BFP8) {
             for (int gg = k0 >> 8; gg < (k1 >> 8); ++gg) mgroup_bfp8<MT, PW>(a, cb, eb, gg, lane, acc);
         } else if (fmt == DR_BFP4) {
             for (int gg = k0 >> 8; gg < (k1 >> 8); ++gg) mgroup_bfp4<MT, PW>(a, cb, eb, gg, lane, acc);
@@ -1609,6 +1833,7 @@ __global__ __launch_bounds__(512) void dr_mfma(const Args a) {
             for (int b0 = k0 / 32; b0 < k1 / 32; b0 += 4) mgroup_bf16<MT, PW>(a, cb, b0, lane, acc);
         }
     }
+    if constexpr (XL) __syncthreads();  // (every wavefront done with its staging before any partial lands on it)
 #pragma unroll
     for (int q = 0; q < PW; ++q)
 #pragma unroll
@@ -2057,9 +2282,10 @@ int rows_per_pass(int m) {
     return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
 }
 
-// dynamic LDS of a dense launch: the partial sums
+// dynamic LDS of a dense launch: the partial sums, and at 32 rows (the MFMA kernel) the wavefronts' x staging
 size_t dense_lds(const Args& a, int pw, int rows) {
-    return (size_t)max(a.waves, a.splits) * pw * rows * 16 * sizeof(float);
+    const size_t part = (size_t)max(a.waves, a.splits) * pw * rows * 16 * sizeof(float);
+    return rows == 32 ? max(part, (size_t)a.waves * XS_BYTES) : part;
 }
 
 template <int MR, int PW>

@@ -276,6 +276,29 @@ def test_narrow_tiles_bitwise(device, fmt):
             same(f"{fmt} K {k} rows {m} 16-column tiles against 32-column tiles", host(both, m, n), alone)
 
 
+@pytest.mark.parametrize("fmt", ["bfp8", "bfp4", "bf16"])
+def test_rows32_staged_x(device, fmt):
+    """Launches of 17 to 32 rows read x through LDS (buffer loads straight to LDS, a swizzled layout, rows past x
+    outside the buffer); launches of 3 to 16 read each operand from x directly. Every output row is its own MFMA row,
+    accumulated in the same order, so the 32-row launch equals, bit for bit, a 16-row launch on its first 16 rows and
+    one on the rest; at a ragged K (the last step's columns past K masked, the last row's past the buffer) and a row
+    count that leaves rows past x, and against the oracle."""
+    n = 320
+    for k in (800, 4096):
+        wt = _special(n, k, 90)
+        tw, _ = linear.native_weight(device, wt, DTYPES[fmt])
+        wk = held(tw, n)
+        for m in (19, 32):
+            x, tx = x_input(device, m, k, 91 + m)
+            assert linear.launch_plan(tx, tw, None)["rows_per_pass"] == 32
+            y = host(linear.matmul(tx, tw, None), m, n)
+            check(f"{fmt} K {k} rows {m}", y, ref(x, wk))
+            lo = host(linear.matmul(tx[..., :16, :].contiguous(), tw, None), 16, n)
+            hi = host(linear.matmul(tx[..., 16:m, :].contiguous(), tw, None), m - 16, n)
+            same(f"{fmt} K {k} rows {m}: rows 0-15 against a 16-row launch", y[:16], lo)
+            same(f"{fmt} K {k} rows {m}: rows 16-{m - 1} against a {m - 16}-row launch", y[16:], hi)
+
+
 def _edge_weights(k, exps, seed, every=1):
     """[16 len(exps), k] weights at the ends of the shared-exponent range: in panel p (16 columns), at every `every`-th
     k, the face row's 16 values are (1 + u) 2^(E - 127), u in [0, 1), random signs, E = exps[p] (the face row's shared

@@ -192,7 +192,8 @@ typedef struct dr_launch_info {
     int32_t passes;        /* launches (row passes) */
     int32_t records;       /* top-k records the launch writes (0: no top-k) */
     int32_t tiles_per_record;
-    int32_t reserved[5];
+    int32_t waves;         /* wavefronts a workgroup (each walks its K chunks in turn) */
+    int32_t reserved[4];
 } dr_launch_info;
 int dr_launch_plan(const dr_launch* launch, dr_launch_info* info);
 

@@ -114,7 +114,8 @@ class LaunchInfo(ctypes.Structure):
         ("passes", c_int32),
         ("records", c_int32),
         ("tiles_per_record", c_int32),
-        ("reserved", c_int32 * 5),
+        ("waves", c_int32),
+        ("reserved", c_int32 * 4),
     ]
 
 

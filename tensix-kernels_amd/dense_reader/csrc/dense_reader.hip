@@ -2761,6 +2761,7 @@ int dr_launch_plan(const dr_launch* L, dr_launch_info* info) {
     info->passes = passes;
     info->records = a.rec != nullptr ? (tiles + a.tk_group - 1) / a.tk_group : 0;
     info->tiles_per_record = a.rec != nullptr ? a.tk_group : 0;
+    info->waves = a.waves;
     return DR_OK;
 }
 

@@ -279,12 +279,12 @@ def test_narrow_tiles_bitwise(device, fmt):
 @pytest.mark.parametrize("fmt", ["bfp8", "bfp4", "bf16"])
 def test_rows32_staged_x(device, fmt):
     """Launches of 17 to 32 rows read x through LDS (buffer loads straight to LDS, a swizzled layout, rows past x
-    outside the buffer); launches of 3 to 16 read each operand from x directly. Every output row is its own MFMA row,
-    accumulated in the same order, so the 32-row launch equals, bit for bit, a 16-row launch on its first 16 rows and
-    one on the rest; at a ragged K (the last step's columns past K masked, the last row's past the buffer) and a row
-    count that leaves rows past x, and against the oracle."""
+    outside the buffer). Every output row is its own MFMA row, accumulated in an order that depends on K and the rows a
+    pass only, so permuting x's rows permutes y's bit for bit: the rows staged in each half of the tile and in each
+    swizzle position land where they belong. At a ragged K (the last step's columns past K masked, the last row's past
+    the buffer), a row count that leaves rows past x, and a K of 256-K chunks (16 wavefronts); against the oracle."""
     n = 320
-    for k in (800, 4096):
+    for k in (800, 4096, 4352):
         wt = _special(n, k, 90)
         tw, _ = linear.native_weight(device, wt, DTYPES[fmt])
         wk = held(tw, n)
@@ -293,10 +293,9 @@ def test_rows32_staged_x(device, fmt):
             assert linear.launch_plan(tx, tw, None)["rows_per_pass"] == 32
             y = host(linear.matmul(tx, tw, None), m, n)
             check(f"{fmt} K {k} rows {m}", y, ref(x, wk))
-            lo = host(linear.matmul(tx[..., :16, :].contiguous(), tw, None), 16, n)
-            hi = host(linear.matmul(tx[..., 16:m, :].contiguous(), tw, None), m - 16, n)
-            same(f"{fmt} K {k} rows {m}: rows 0-15 against a 16-row launch", y[:16], lo)
-            same(f"{fmt} K {k} rows {m}: rows 16-{m - 1} against a {m - 16}-row launch", y[16:], hi)
+            perm = torch.cat([torch.arange(m - 1, 15, -1), torch.arange(16)[torch.randperm(16, generator=torch.Generator().manual_seed(m))]])
+            yp = host(linear.matmul(tx[..., perm.to(tx.device), :].contiguous(), tw, None), m, n)
+            same(f"{fmt} K {k} rows {m}: rows permuted", yp, y[perm])
 
 
 def _edge_weights(k, exps, seed, every=1):

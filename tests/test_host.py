@@ -52,10 +52,10 @@ def test_struct_layout_matches_c(tmp_path):
     src = tmp_path / "layout.c"
     src.write_text(
         '#include <stdio.h>\n#include <stddef.h>\n#include "dense_reader.h"\n'
-        "int main(void){printf(\"%zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\\n\", sizeof(dr_segment), sizeof(dr_topk),"
+        "int main(void){printf(\"%zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\\n\", sizeof(dr_segment), sizeof(dr_topk),"
         " sizeof(dr_launch), offsetof(dr_launch, seg), offsetof(dr_launch, topk), offsetof(dr_launch, stream),"
         " offsetof(dr_topk, base), offsetof(dr_segment, col0), offsetof(dr_launch, workspace_bytes),"
-        " sizeof(dr_launch_info), offsetof(dr_launch_info, tiles_per_record));return 0;}\n"
+        " sizeof(dr_launch_info), offsetof(dr_launch_info, tiles_per_record), offsetof(dr_launch_info, waves));return 0;}\n"
     )
     exe = tmp_path / "layout"
     subprocess.run(["gcc", "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
@@ -72,6 +72,7 @@ def test_struct_layout_matches_c(tmp_path):
         _lib.Launch.workspace_bytes.offset,
         ctypes.sizeof(_lib.LaunchInfo),
         _lib.LaunchInfo.tiles_per_record.offset,
+        _lib.LaunchInfo.waves.offset,
     ]
     assert got == want
 
@@ -135,10 +136,11 @@ def test_launch_plan_on_the_host():
     MFMA kernel, a long K split, top-k records one a tile; an invalid launch is refused."""
     p = _lib.launch_info(_ns_launch())
     assert (p["kernel"], p["rows_per_pass"], p["tile_cols"], p["tiles"], p["splits"]) == ("gemv", 1, 32, 448, 1), p
+    assert p["waves"] == 8 and p["chunks"] == 8, p
     p = _lib.launch_info(_ns_launch(m=32))
-    assert (p["kernel"], p["rows_per_pass"], p["passes"]) == ("mfma", 32, 1), p
+    assert (p["kernel"], p["rows_per_pass"], p["passes"], p["chunks"], p["kch"], p["waves"]) == ("mfma", 32, 1, 8, 512, 8), p
     p = _lib.launch_info(_ns_launch(m=8, k=14336, n=4096))
-    assert (p["kernel"], p["rows_per_pass"], p["splits"], p["chunks"], p["kch"]) == ("mfma", 16, 2, 28, 512), p
+    assert (p["kernel"], p["rows_per_pass"], p["splits"], p["chunks"], p["kch"], p["waves"]) == ("mfma", 16, 2, 28, 512, 8), p
     p = _lib.launch_info(_ns_launch(n=1000))
     assert (p["tile_cols"], p["tiles"]) == (16, 63), p  # few tiles: 16-column tiles
     info = _lib.LaunchInfo()

@@ -1255,12 +1255,16 @@ __global__ __launch_bounds__(512) void dr_gemv_moe(const MoeArgs a) {
                 wsum[q][m] += bfp4_chunk_sum(v, c);
             }
     };
+    // DR_MOE_DOWN: every slot's id, lane j slot j, read once (a chunk then takes its unit's id from a lane, not from
+    // memory: one dependent round trip fewer a chunk)
+    int idv = -1;
+    if constexpr (MOE == DR_MOE_DOWN) idv = lane < a.slots ? moe_id(a, 0, lane) : -1;
     const int ch1 = min((split + 1) * a.cps, a.chunks);
     for (int ch = split * a.cps + wave; ch < ch1; ch += a.waves) {
         const int k0 = ch * a.kch, k1 = min(k0 + a.kch, a.k_pad);
         if constexpr (moe_k<MOE>()) {
-            const int s = k0 / a.ekp;
-            int e = MOE == DR_MOE_DOWN ? moe_id(a, 0, s) : (s < ul->count ? (int)ul->list[s] : -1);
+            const int s = __builtin_amdgcn_readfirstlane(k0 / a.ekp);
+            int e = MOE == DR_MOE_DOWN ? __builtin_amdgcn_readlane(idv, s) : (s < ul->count ? (int)ul->list[s] : -1);
             e = __builtin_amdgcn_readfirstlane(e);
             if (e < 0) continue;  // (an id past the experts, or a block past the union: nothing to add)
             Args b = a;  // (the chunk's view of x: the unit's block)
@@ -1899,12 +1903,16 @@ __global__ __launch_bounds__(512) void dr_mfma_moe(const MoeArgs a) {
                 mgroup_bfp4<MT, PW>(b, cbx, ebx, gg, lane, acc);
         }
     };
+    // DR_MOE_DOWN: every slot's id, lane j slot j, read once (a chunk then takes its unit's id from a lane, not from
+    // memory: one dependent round trip fewer a chunk)
+    int idv = -1;
+    if constexpr (MOE == DR_MOE_DOWN) idv = lane < a.slots ? moe_id(a, 0, lane) : -1;
     const int ch1 = min((split + 1) * a.cps, a.chunks);
     for (int ch = split * a.cps + wave; ch < ch1; ch += a.waves) {
         const int k0 = ch * a.kch, k1 = min(k0 + a.kch, a.k_pad);
         if constexpr (moe_k<MOE>()) {
-            const int s = k0 / a.ekp;
-            int e = MOE == DR_MOE_DOWN ? moe_id(a, 0, s) : (s < ul->count ? (int)ul->list[s] : -1);
+            const int s = __builtin_amdgcn_readfirstlane(k0 / a.ekp);
+            int e = MOE == DR_MOE_DOWN ? __builtin_amdgcn_readlane(idv, s) : (s < ul->count ? (int)ul->list[s] : -1);
             e = __builtin_amdgcn_readfirstlane(e);
             if (e < 0) continue;
             Args b = a;  // (the chunk's view of x: the unit's block)
@@ -2870,9 +2878,11 @@ int prepare_moe(const dr_launch* L, const dr_moe* M, MoeArgs& a, int& pw, int& t
         a.seg[0].pstride = (unsigned)((ekp / kblk(DR_BFP4)) * 1024);
         if (ekp % a.kch) plan_chunks(a.k_pad, 256, &a.chunks, &a.kch, &a.waves, &a.splits, &a.cps);  // (a chunk in one unit)
         // The GEMV's tile width and K splits (the down modes have no block lists, so they may depend on N): the pair
-        // that lowers the most any CU streams, ceil(workgroups / CUs) workgroups of cps chunks x the width each; ties
-        // to fewer splits, then to 32 columns (the gpt-oss-shaped down, 90 tiles x 24 chunks: 16 columns in 4 splits of
-        // 6 chunks, 720 workgroups, against 32 columns in 2 splits, 180 workgroups on 256 CUs).
+        // of the lowest cost, ceil(workgroups / CUs) rounds of cps chunks x the width each plus a workgroup's fixed
+        // cost (its start, barrier and epilogue: about two 16-column chunks), plus the splits' meeting (about four);
+        // ties to fewer splits, then to 32 columns. The gpt-oss-shaped down, 90 tiles x 24 chunks: 16 columns unsplit,
+        // 180 workgroups of 3 chunks a wavefront (7.4 us; in 4 splits of 6 chunks, 720 workgroups, 8.0 us, the
+        // choice without those terms; 2 splits 8.2, 3 8.1).
         if (mr <= 2) {
             const int c = cu_count(), t32 = a.seg[0].tiles, t16 = (a.seg[0].n_out + 15) / 16;
             long best = -1;
@@ -2882,7 +2892,7 @@ int prepare_moe(const dr_launch* L, const dr_moe* M, MoeArgs& a, int& pw, int& t
                 for (int w = 16; w <= 32; w += 16) {
                     const long wg = (long)(w == 16 ? t16 : t32) * sp;
                     if ((w == 16 ? t16 : t32) > SPLIT_MAXTILES) continue;
-                    const long cost = (wg + c - 1) / c * cps * w;
+                    const long cost = (wg + c - 1) / c * ((long)cps * w + 32) + (sp > 1 ? 64 : 0);
                     if (best < 0 || cost < best || (cost == best && (sp < (a.chunks + bcps - 1) / bcps ||
                                                                      (sp == (a.chunks + bcps - 1) / bcps && w > bw)))) {
                         best = cost;

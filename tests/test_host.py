@@ -143,8 +143,19 @@ def test_launch_plan_on_the_host():
     assert (p["kernel"], p["rows_per_pass"], p["splits"], p["chunks"], p["kch"], p["waves"]) == ("mfma", 16, 2, 28, 512, 8), p
     p = _lib.launch_info(_ns_launch(n=1000))
     assert (p["tile_cols"], p["tiles"]) == (16, 63), p  # few tiles: 16-column tiles
+    # the split-K workspace has counters for 16384 tiles: a launch of more runs unsplit (its workgroups walk all 28
+    # chunks), one at the limit still splits
+    p = _lib.launch_info(_ns_launch(m=8, k=14336, n=32 * 16384))
+    assert (p["tiles"], p["splits"], p["chunks"]) == (16384, 2, 28), p
+    p = _lib.launch_info(_ns_launch(m=8, k=14336, n=32 * 16385))
+    assert (p["tiles"], p["splits"], p["chunks"], p["waves"]) == (16385, 1, 28, 8), p
     info = _lib.LaunchInfo()
     assert _lib.lib().dr_launch_plan(ctypes.byref(_lib.Launch()), ctypes.byref(info)) == _lib.DR_EINVAL
+    # empty shapes and a K that is not a multiple of 32 are refused; more than 32 rows run in passes of 32
+    for bad in ({"m": 0}, {"k": 0}, {"n": 0}, {"k": 8}, {"k": 33}):
+        assert _lib.lib().dr_launch_plan(ctypes.byref(_ns_launch(**bad)), ctypes.byref(info)) == _lib.DR_EINVAL, bad
+    p = _lib.launch_info(_ns_launch(m=100))
+    assert (p["rows_per_pass"], p["passes"]) == (32, 4), p
 
 
 class _FakeWeight:

@@ -193,7 +193,9 @@ typedef struct dr_launch_info {
     int32_t records;       /* top-k records the launch writes (0: no top-k) */
     int32_t tiles_per_record;
     int32_t waves;         /* wavefronts a workgroup (each walks its K chunks in turn) */
-    int32_t reserved[4];
+    int32_t tiles_per_workgroup; /* 2: a 32-row launch of more tiles than CUs, its block-float segments' tiles in
+                                    pairs (bf16 segments one a workgroup), else 1 */
+    int32_t reserved[3];
 } dr_launch_info;
 int dr_launch_plan(const dr_launch* launch, dr_launch_info* info);
 

@@ -115,7 +115,8 @@ class LaunchInfo(ctypes.Structure):
         ("records", c_int32),
         ("tiles_per_record", c_int32),
         ("waves", c_int32),
-        ("reserved", c_int32 * 4),
+        ("tiles_per_workgroup", c_int32),
+        ("reserved", c_int32 * 3),
     ]
 
 

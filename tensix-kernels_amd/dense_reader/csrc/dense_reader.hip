@@ -117,6 +117,9 @@ struct Args {
     int splits, cps, tiles;  // split K: splits workgroups a tile, cps chunks each; tiles of the launch
     uint32_t* counters;      // [tiles] (splits > 1): workgroups of the tile done, reset to 0 by the last
     float* wpart;            // [tiles][splits][PW * ROWS * 16] (splits > 1): each workgroup's column sums
+    int pairs;               // > 0: 32-row launch of tile pairs (dr_mfma_pairs), this many workgroups
+    int pair_begin[4];       // each segment's first workgroup
+    int pair_tiles[4];       // each segment's tiles a workgroup (2, or 1 for bf16)
 };
 
 // the expert-gathered launches' arguments (DR_MOE_*): the workgroup's expert (gate/up modes) or each chunk's (down
@@ -1851,6 +1854,80 @@ __global__ __launch_bounds__(512, MT == 2 ? 4 : 1) void dr_mfma(const Args a) { 
     if (nparts) epilogue<ROWS, PW>(a, sg, t, part, nparts, tval, tkey, wave, lane, pre);
 }
 
+// ---- 32 rows, two tiles a workgroup -------------------------------------------------------------------------------
+//
+// A 32-row launch of more tiles than CUs: each workgroup of a block-float segment computes two adjacent 32-column
+// tiles (the last pair of an odd count, one). Its wavefronts stage their x once for four panels, so x's traffic into
+// the CU and the workgroup's fixed cost (its start, barriers, epilogue) are paid once a pair, and the launch has fewer
+// workgroups (C4's 192 bfloat8_b tiles: 96, beside the 128 bf16 tiles: 224 workgroups, one round on 256 CUs, where 64
+// CUs had had two tiles one after the other). bf16 segments keep a tile a workgroup: their weights are twice x's bytes
+// a tile, and pairing them halved the workgroups for little saved (the NS shape at 32 rows: 28.2 -> 29.9 us, against
+// bfloat8_b's 21.5 -> 19.6). Each tile's panels are summed by the same lanes, steps and wavefronts in the same order as
+// in dr_mfma<2, 2>, so the results are the same bit for bit. Plain tiles only: no top-k records, GLU, residual or
+// split K.
+template <int PW, int FMT>  // PW 4: two tiles, 2: one
+__device__ __forceinline__ void pair_tiles(const Args& a, const SegDev& sg, int t0, int nt, int fmt, int wave,
+                                           int lane, float* part, float (*tval)[TILE], uint32_t (*tkey)[TILE]) {
+    constexpr int ROWS = 32;
+    const uint8_t* cb[PW];
+    const uint8_t* eb[PW];
+#pragma unroll
+    for (int q = 0; q < PW; ++q) {
+        const int pan = 2 * (t0 + (nt == 2 ? q >> 1 : 0)) + (q & 1);
+        cb[q] = sg.codes + (size_t)pan * sg.pstride;
+        eb[q] = sg.exps + (size_t)pan * a.k_pad;
+    }
+    f32x4 acc[PW][2];
+#pragma unroll
+    for (int q = 0; q < PW; ++q)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) acc[q][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    uint4* xs = reinterpret_cast<uint4*>(part) + wave * (XS_BYTES / 16);
+    for (int ch = wave; ch < a.chunks; ch += a.waves) {
+        const int k0 = ch * a.kch, k1 = min(k0 + a.kch, a.k_pad);
+        if (fmt == DR_BFP8) xl_chunk_bfp8<PW>(a, cb, eb, k0, k1, lane, acc, xs);
+        else if (fmt == DR_BFP4) xl_chunk_bfp4<PW>(a, cb, eb, k0, k1, lane, acc, xs);
+        else xl_chunk_bf16<PW>(a, cb, k0, k1, lane, acc, xs);
+    }
+    __syncthreads();  // (every wavefront done with its staging before any partial lands on it)
+    const int W = a.waves;
+#pragma unroll
+    for (int q = 0; q < PW; ++q)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                part[((((q >> 1) * W + wave) * 2 + (q & 1)) * ROWS + 16 * tt + 4 * (lane >> 4) + j) * 16 + (lane & 15)] =
+                    acc[q][tt][j];
+    __syncthreads();
+    for (int u = 0; u < PW / 2 && u < nt; ++u)
+        epilogue<ROWS, 2>(a, sg, t0 + u, part + (size_t)u * W * 2 * ROWS * 16, W, tval, tkey, wave, lane);
+}
+
+template <int FMT, bool ONE>
+__global__ __launch_bounds__(512) void dr_mfma_pairs(const Args a) {
+    extern __shared__ float part[];  // x staging during the K loop; then [tiles][W][2][32][16]
+    __shared__ float tval[32][TILE];
+    __shared__ uint32_t tkey[32][TILE];
+    const int gp = blockIdx.x;
+    int si = 0;
+    if (!ONE) {
+#pragma unroll
+        for (int j = 1; j < 4; ++j)
+            if (j < a.nseg && gp >= a.pair_begin[j]) si = j;
+    }
+    const SegDev& sg = a.seg[si];
+    const int per = a.pair_tiles[si];  // (uniform)
+    const int t0 = per * (gp - a.pair_begin[si]);
+    const int nt = sg.tiles - t0 < per ? sg.tiles - t0 : per;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int fmt = FMT >= 0 ? FMT : sg.fmt;
+    if (nt == 2)
+        pair_tiles<4, FMT>(a, sg, t0, nt, fmt, wave, lane, part, tval, tkey);
+    else
+        pair_tiles<2, FMT>(a, sg, t0, nt, fmt, wave, lane, part, tval, tkey);
+}
+
 template <int MT, int PW, int MOE, bool KB>
 __global__ __launch_bounds__(512) void dr_mfma_moe(const MoeArgs a) {
     constexpr int ROWS = 16 * MT;
@@ -2387,7 +2464,25 @@ hipError_t launch_moe(const MoeArgs& a, int mode, int rows, int pw, int grid, hi
 }
 
 // one pass of up to `rows` rows
+void launch_pairs(const Args& a, hipStream_t st) {
+    const dim3 b(64 * a.waves);
+    const size_t lds = max((size_t)a.waves * XS_BYTES, (size_t)2 * a.waves * 2 * 32 * 16 * sizeof(float));
+    if (a.nseg > 1) {
+        hipLaunchKernelGGL((dr_mfma_pairs<-1, false>), dim3(a.pairs), b, lds, st, a);
+        return;
+    }
+    switch (a.seg[0].fmt) {
+        case DR_BFP8: hipLaunchKernelGGL((dr_mfma_pairs<DR_BFP8, true>), dim3(a.pairs), b, lds, st, a); break;
+        case DR_BFP4: hipLaunchKernelGGL((dr_mfma_pairs<DR_BFP4, true>), dim3(a.pairs), b, lds, st, a); break;
+        default: hipLaunchKernelGGL((dr_mfma_pairs<DR_BF16, true>), dim3(a.pairs), b, lds, st, a); break;
+    }
+}
+
 hipError_t launch_rows(const Args& a, int rows, int pw, int grid, hipStream_t st) {
+    if (rows == 32 && a.pairs > 0) {
+        launch_pairs(a, st);
+        return hipGetLastError();
+    }
     switch (rows) {
         case 1: pw == 1 ? launch_gemv<1, 1>(a, grid, st) : pw == 2 ? launch_gemv<1, 2>(a, grid, st) : launch_gemv<1, 4>(a, grid, st); break;
         case 2: pw == 1 ? launch_gemv<2, 1>(a, grid, st) : pw == 2 ? launch_gemv<2, 2>(a, grid, st) : launch_gemv<2, 4>(a, grid, st); break;
@@ -2607,6 +2702,18 @@ int prepare(const dr_launch* L, Args& a, int& pw, int& tiles, int& mr, bool gath
         plan(L->k, &a.chunks, &a.kch, &a.waves, &a.splits, &a.cps);
         limit_splits(a);
     }
+    // 32 rows, plain tiles, more tiles than CUs: block-float segments in tile pairs (dr_mfma_pairs)
+    a.pairs = 0;
+    bool pairable = false;
+    for (int i = 0; i < a.nseg; ++i) pairable |= a.seg[i].fmt != DR_BF16;
+    if (!gather && pairable && mr == 32 && pw == 2 && a.splits == 1 && a.rec == nullptr && a.res == nullptr &&
+        tiles > cu_count()) {
+        for (int i = 0; i < a.nseg; ++i) {
+            a.pair_tiles[i] = a.seg[i].fmt == DR_BF16 ? 1 : 2;
+            a.pair_begin[i] = a.pairs;
+            a.pairs += (a.seg[i].tiles + a.pair_tiles[i] - 1) / a.pair_tiles[i];
+        }
+    }
     return DR_OK;
 }
 
@@ -2762,7 +2869,8 @@ int dr_launch_plan(const dr_launch* L, dr_launch_info* info) {
     info->chunks = a.chunks;
     info->kch = a.kch;
     info->splits = a.splits;
-    info->workgroups = tiles * a.splits;
+    info->workgroups = a.pairs > 0 ? a.pairs : tiles * a.splits;
+    info->tiles_per_workgroup = a.pairs > 0 ? 2 : 1;  // (block-float segments; a launch's bf16 segments take 1)
     int passes = 0;
     for (int r0 = 0; r0 < L->m; r0 += mr)
         if (!(a.rec != nullptr && r0 >= a.tk_rows && !a.write_y)) ++passes;

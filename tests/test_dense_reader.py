@@ -298,6 +298,41 @@ def test_rows32_staged_x(device, fmt):
             same(f"{fmt} K {k} rows {m}: rows permuted", yp, y[perm])
 
 
+def test_rows32_tile_pairs(device):
+    """A 32-row launch of more tiles than CUs runs its block-float segments' tiles in pairs, a workgroup each (the
+    last of an odd count alone), and its bf16 segments' one a workgroup: a block list of bfloat8_b (129 tiles, odd),
+    bf16 (64) and bfloat4_b (65, odd), 258 tiles, equals one call per block bit for bit (each alone has fewer tiles
+    than CUs: no pairs), with scales on the first block and 19 rows (rows past x), and the oracle."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    k, m = 768, 19
+    spec = [("bfp8", 129), ("bf16", 64), ("bfp4", 65)]
+    extra = max(0, cus + 2 - sum(t for _, t in spec))  # (more tiles than this box's CUs)
+    spec[1] = ("bf16", spec[1][1] + extra)
+    x, tx = x_input(device, m, k, 120)
+    blocks, col0, parts = [], 0, []
+    sc = linear.scale_tensor(device, torch.rand(32 * spec[0][1], generator=torch.Generator().manual_seed(121)) + 0.5,
+                             dtype=linear.float32)
+    for i, (fmt, tiles) in enumerate(spec):
+        n = 32 * tiles
+        wt = matrix(n, k, 122 + i)
+        tw, _ = linear.native_weight(device, wt, DTYPES[fmt])
+        blocks.append((tw, col0 // 32, sc) if i == 0 else (tw, col0 // 32))
+        parts.append((tw, n, col0, sc if i == 0 else None))
+        col0 += n
+    p = linear.launch_plan(tx, blocks, None)
+    assert (p["kernel"], p["rows_per_pass"], p["tiles_per_workgroup"]) == ("mfma", 32, 2), p
+    assert p["workgroups"] == 65 + spec[1][1] + 33, p
+    y = host(linear.matmul(tx, blocks, None), m, col0)
+    for tw, n, c0, s in parts:
+        assert linear.launch_plan(tx, tw, s)["tiles_per_workgroup"] == 1
+        alone = host(linear.matmul(tx, tw, s), m, n)
+        same(f"{tw.dtype} block of {n} columns against its own call", y[:, c0 : c0 + n], alone)
+        want = ref(x, held(tw, n))
+        if s is not None:
+            want = want * s.float().cpu().reshape(1, -1)
+        check(f"{tw.dtype} block of {n} columns", alone, want)
+
+
 def _edge_weights(k, exps, seed, every=1):
     """[16 len(exps), k] weights at the ends of the shared-exponent range: in panel p (16 columns), at every `every`-th
     k, the face row's 16 values are (1 + u) 2^(E - 127), u in [0, 1), random signs, E = exps[p] (the face row's shared

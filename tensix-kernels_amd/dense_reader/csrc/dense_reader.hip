@@ -916,17 +916,18 @@ __device__ __forceinline__ void epilogue(const Args& a, const SegDev& sg, int t,
     }
     if (!topk) return;
     __syncthreads();
-    // one wavefront ranks each row's 32 keys: the best k, highest first, ties to the lower column. The record goes to
-    // its slot, or with grouped records to the tile's staging record (dr_group_k ranks the groups afterwards).
-    if (wave == 0) {
+    // the workgroup's wavefronts rank the rows, two a wavefront (a 32-lane half each; one wavefront walking every row in
+    // turn had kept the workgroup ≈ 1 µs a 4-row tile: C5's records cost 19 of its 103 µs): each row's 32 keys, the
+    // best k, highest first, ties to the lower column. The record goes to its slot, or with grouped records to the
+    // tile's staging record (dr_group_k ranks the groups afterwards).
+    {
         const int K = a.tk_k, R = a.tk_rows;
         const size_t rlen = 2 * (size_t)R * K;
         uint32_t* rec = a.rec_out + (size_t)t * rlen;
         auto put = [](uint32_t* p, uint32_t v) { *p = v; };
-        for (int m = 0; m < mrows; ++m) {
+        const int nw = (int)(blockDim.x >> 6), c = lane & 31;
+        for (int m = 2 * wave + (lane >> 5); m < mrows && a.row0 + m < R; m += 2 * nw) {
             const int r = a.row0 + m;
-            if (r >= R) break;
-            const int c = lane & 31;
             const uint32_t key = tkey[m][c];
             // rank: the columns ahead of c, by key then the lower column first (one 64-bit compare a column: the
             // key above the column complemented)
@@ -938,14 +939,14 @@ __device__ __forceinline__ void epilogue(const Args& a, const SegDev& sg, int t,
                 nval += kj != 0u;
                 rank += (((unsigned long long)kj << 32) | (uint32_t)(TILE - 1 - j)) > me;
             }
-            if (lane < 32 && key != 0u && rank < K) {
+            if (key != 0u && rank < K) {
                 const float val = tval[m][c];
                 put(rec + (size_t)r * K + rank, a.tk_fp32 ? __float_as_uint(val) : key);
                 put(rec + (size_t)R * K + (size_t)r * K + rank, (uint32_t)(a.base + (long long)t * TILE + c));
             }
-            if (lane >= nval && lane < K) {
-                put(rec + (size_t)r * K + lane, a.tk_fp32 ? 0xFF800000u : 0u);
-                put(rec + (size_t)R * K + (size_t)r * K + lane, 0xFFFFFFFFu);
+            if (c >= nval && c < K) {
+                put(rec + (size_t)r * K + c, a.tk_fp32 ? 0xFF800000u : 0u);
+                put(rec + (size_t)R * K + (size_t)r * K + c, 0xFFFFFFFFu);
             }
         }
     }

@@ -214,13 +214,40 @@ __device__ __forceinline__ unsigned long long lane_value(unsigned long long v, i
     return ((unsigned long long)hi << 32) | lo;
 }
 
+// the largest t with at least k lanes holding m >= t (k <= 64; 0 when no larger t has k): the k-th largest m over the
+// wavefront, found bit by bit from the top with one ballot a bit
+__device__ __forceinline__ uint32_t wave_kth_largest(uint32_t m, int k) {
+    uint32_t t = 0u;
+#pragma unroll
+    for (int b = 31; b >= 0; --b) {
+        const uint32_t c = t | (1u << b);
+        if (__popcll(__ballot(m >= c)) >= k) t = c;
+    }
+    return t;
+}
+
 // A wavefront's running best: list (sorted decreasing over the lanes; NARROW, k_out <= 32: over lanes 0-31 only), thr
-// its k_out-th value (only larger candidates can enter), and up to 64 entrants waiting in pend (LDS) to be sorted and
-// merged in at once.
+// its k_out-th value or the floor, whichever is larger (only larger candidates can enter), and up to 64 entrants
+// waiting in pend (LDS) to be sorted and merged in at once.
 template <bool NARROW>
 struct WaveBest {
-    unsigned long long list = 0ull, thr = 0ull;
+    unsigned long long list = 0ull, thr = 0ull, floor = 0ull;
     int count = 0;
+
+    // v: this lane's candidates of the first load round (U a lane, 0: none). The k_out-th largest of the lanes'
+    // largest high words, t, has k_out lanes holding a candidate at or above t << 32, so a candidate below it is
+    // beaten by k_out others and cannot be among the best k_out: most candidates stay out of the sorts from the start.
+    template <int U>
+    __device__ __forceinline__ void raise_floor(const unsigned long long (&v)[U], int kout) {
+        uint32_t m = 0u;
+#pragma unroll
+        for (int u = 0; u < U; ++u) m = max(m, (uint32_t)(v[u] >> 32));
+        const uint32_t t = wave_kth_largest(m, kout);
+        if (t != 0u) {
+            floor = ((unsigned long long)t << 32) - 1ull;  // (entry: v > thr)
+            thr = thr > floor ? thr : floor;
+        }
+    }
 
     __device__ __forceinline__ void flush(unsigned long long* pend, int kout, int lane) {
         if (count == 0) return;
@@ -232,6 +259,7 @@ struct WaveBest {
         else
             list = wave_merge(list, up, lane);
         thr = lane_value(list, kout - 1);
+        thr = thr > floor ? thr : floor;
         count = 0;
         __builtin_amdgcn_wave_barrier();
     }
@@ -346,6 +374,7 @@ __device__ __forceinline__ bool select_row(const SelArgs& A, int r, int sl, Comp
                 v[u] = c[u] < c1 ? comp(key[u], id[u], (uint32_t)c[u]) : 0ull;
                 n += __popcll(__ballot(v[u] != 0ull));  // (the wavefront's count, uniform)
             }
+            if (b0 == wave) best.raise_floor(v, A.keep);  // (the first round)
 #pragma unroll
             for (int u = 0; u < 4; ++u) best.add(v[u], sh.pend[wave], A.keep, lane);
         }

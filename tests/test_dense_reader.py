@@ -493,6 +493,32 @@ def test_topk_merge_synthetic(device, fp32):
         same(f"merge ids nrec {nrec} rows {rows} k {k} k_out {k_out}", ids.cpu().long(), torch.from_numpy(wi))
 
 
+def test_topk_merge_ordered(device):
+    """Records whose values rise or fall with the slot (the best all in the first or last loads of a slice, or in a
+    few lanes of a load), so a wavefront's early threshold comes from the fewest lanes possible: against the oracle's
+    host merge."""
+    nrec, rows, k = 4008, 2, 8
+    base = np.arange(nrec * k, dtype=np.float32) / 64.0
+    for name, v in (("rising", base), ("falling", base[::-1].copy()),
+                    ("a few lanes", np.where(np.arange(nrec * k) % 64 < 3, base, -base))):
+        vals = np.stack([v, v[::-1]], axis=1).reshape(nrec, k, rows).transpose(0, 2, 1)  # [nrec, rows, k]
+        ids = (np.arange(nrec * rows * k, dtype=np.int64).reshape(nrec, rows, k) * 7919) % (1 << 30)
+        for fp32 in (False, True):
+            if fp32:
+                keys = vals.astype(np.float32).view(np.uint32).astype(np.int64)
+            else:
+                keys = O.key_bf16(O.bf16_bits(torch.from_numpy(np.ascontiguousarray(vals, np.float32))))
+            words = np.concatenate([keys.reshape(nrec, rows * k), ids.reshape(nrec, rows * k)], axis=1)
+            t = torch.from_numpy((words & 0xFFFFFFFF).astype(np.uint32).view(np.int32))
+            hv, hi = linear.records_host(t, rows, k, fp32=fp32)
+            r = t.reshape(1, 1, nrec, -1).to(device.torch)
+            for k_out in (32, 64):
+                wv, wi = O.global_topk(hv.numpy(), hi.numpy(), k_out)
+                gv, gi = linear.topk_merge(r, rows, k, k_out=k_out, fp32=fp32)
+                same(f"merge values {name} fp32 {fp32} k_out {k_out}", gv.cpu(), torch.from_numpy(wv))
+                same(f"merge ids {name} fp32 {fp32} k_out {k_out}", gi.cpu().long(), torch.from_numpy(wi))
+
+
 @pytest.mark.parametrize("fmt", ["bfp8", "bfp4", "bf16"])
 def test_split_k(device, fmt):
     """A K long enough to be split over several workgroups a tile (they meet in the workspace): against the oracle,

@@ -766,6 +766,11 @@ struct UnionLds {
     int count;
 };
 
+// the workgroup's threads: every launch of these kernels has 64 * a.waves. (blockDim.x reads the dispatch's implicit
+// arguments, on a line of the argument block nothing else touches: in an epilogue, a scalar-cache miss and a round
+// trip after the K loop.)
+__device__ __forceinline__ int wg_threads(const Args& a) { return 64 * a.waves; }
+
 template <int MOE>
 __device__ __forceinline__ UnionLds* union_lds() {
     __shared__ UnionLds u;
@@ -774,9 +779,9 @@ __device__ __forceinline__ UnionLds* union_lds() {
 
 // every thread of the workgroup calls it: a bitmap of the ids, then wavefront 0 lists its set bits in order
 __device__ __forceinline__ void moe_union(const MoeArgs& a, UnionLds& u) {
-    for (int i = threadIdx.x; i < 32; i += blockDim.x) u.bits[i] = 0u;
+    for (int i = threadIdx.x; i < 32; i += wg_threads(a)) u.bits[i] = 0u;
     __syncthreads();
-    for (int i = threadIdx.x; i < a.id_rows * a.slots; i += blockDim.x) {
+    for (int i = threadIdx.x; i < a.id_rows * a.slots; i += wg_threads(a)) {
         const int e = moe_id(a, i / a.slots, i % a.slots);
         if (e >= 0) atomicOr(&u.bits[e >> 5], 1u << (e & 31));
     }
@@ -856,7 +861,7 @@ __device__ __forceinline__ void epilogue(const Args& a, const SegDev& sg, int t,
     constexpr int TW = tile_w<PW>();
     const int mrows = min(a.m, ROWS);
     const bool topk = a.rec != nullptr;  // (never with PW = 1)
-    for (int e = threadIdx.x; e < TW * ROWS; e += blockDim.x) {
+    for (int e = threadIdx.x; e < TW * ROWS; e += wg_threads(a)) {
         const int m = e / TW, col = e % TW;
         const int oc = t * TW + col;  // output column of this segment
         const bool valid = m < mrows && oc < sg.n_out;
@@ -925,7 +930,7 @@ __device__ __forceinline__ void epilogue(const Args& a, const SegDev& sg, int t,
         const size_t rlen = 2 * (size_t)R * K;
         uint32_t* rec = a.rec_out + (size_t)t * rlen;
         auto put = [](uint32_t* p, uint32_t v) { *p = v; };
-        const int nw = (int)(blockDim.x >> 6), c = lane & 31;
+        const int nw = a.waves, c = lane & 31;
         for (int m = 2 * wave + (lane >> 5); m < mrows && a.row0 + m < R; m += 2 * nw) {
             const int r = a.row0 + m;
             const uint32_t key = tkey[m][c];
@@ -976,7 +981,7 @@ __device__ __forceinline__ void epilogue_moe(const MoeArgs& a, int t, int unit, 
         coef[m] = c;
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < TW * ROWS; e += blockDim.x) {
+    for (int e = threadIdx.x; e < TW * ROWS; e += wg_threads(a)) {
         const int m = e / TW, col = e % TW;
         const int oc = t * TW + col;  // the column within the expert's
         if (m >= mrows || oc >= a.en) continue;
@@ -999,7 +1004,7 @@ __device__ __forceinline__ void epilogue_moe(const MoeArgs& a, int t, int unit, 
 template <int PW>
 __device__ __forceinline__ void moe_zero(const MoeArgs& a, int t, int unit) {
     constexpr int TW = 8 * PW;
-    for (int col = threadIdx.x; col < TW; col += blockDim.x) {
+    for (int col = threadIdx.x; col < TW; col += wg_threads(a)) {
         const int oc = t * TW + col;
         if (oc < a.en) reinterpret_cast<uint16_t*>(a.y)[(size_t)unit * a.en + oc] = 0;
     }
@@ -1038,7 +1043,7 @@ __device__ __forceinline__ int gather_splits(const Args& a, int g, int split, fl
     __shared__ int last;
     if (a.splits == 1) return a.waves;
     float* mine = a.wpart + ((size_t)g * a.splits + split) * E;
-    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    for (int e = threadIdx.x; e < E; e += wg_threads(a)) {
         float v = 0.f;
         for (int w = 0; w < a.waves; ++w) v += part[w * E + e];
         st_dev(mine + e, v);
@@ -1050,7 +1055,7 @@ __device__ __forceinline__ int gather_splits(const Args& a, int g, int split, fl
     __syncthreads();
     if (!last) return 0;
     const float* all = a.wpart + (size_t)g * a.splits * E;
-    for (int e = threadIdx.x; e < a.splits * E; e += blockDim.x) part[e] = ld_dev(all + e);
+    for (int e = threadIdx.x; e < a.splits * E; e += wg_threads(a)) part[e] = ld_dev(all + e);
     if (threadIdx.x == 0) __hip_atomic_store(a.counters + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     return a.splits;

@@ -3,10 +3,12 @@
 The config tests pin each benchmarked shape; this sweep covers the combinations between them: formats, rows on either
 kernel (1-2 GEMV, 3-32 MFMA, past 32 in passes), K with and without padding and split K, N off the tile width, bf16
 and fp32 column scales, the GLU (interleaved or two weights, silu or gelu_tanh, with or without scales), the residual
-in both modes with and without the fp32 output, the fp32 output alone, col0 into a wider output, and block lists of
-mixed formats with per-block scales. Expected values come from the oracle alone (oracle.held of the float weights,
-oracle.ref in float64), with the reference's bars (linear.py / test_dense_reader.py: 1 % relative Frobenius error and
-PCC 0.9999 for bf16 outputs, 0.1 % for fp32 outputs); every case is also called twice and must repeat bit for bit.
+in both modes with and without the fp32 output, the fp32 output alone, col0 into a wider output, block lists of mixed
+formats with per-block scales, and top-k records (bf16 keys, a record a tile or groups of tiles). Expected values come
+from the oracle alone (oracle.held of the float weights, oracle.ref in float64, oracle.tile_topk's ranking of the op's
+own output), with the reference's bars (linear.py / test_dense_reader.py: 1 % relative Frobenius error and PCC 0.9999
+for bf16 outputs, 0.1 % for fp32 outputs, records bit for bit); every case is also called twice and must repeat bit
+for bit.
 """
 
 import numpy as np
@@ -23,7 +25,7 @@ FMTS = {"bfp8": linear.bfloat8_b, "bfp4": linear.bfloat4_b, "bf16": linear.bfloa
 KS = (96, 256, 480, 1024, 1056, 2048, 2080, 4096, 4352, 6144, 9216)
 NS_ = (32, 48, 96, 200, 256, 480, 544, 1024, 1056)
 MS = (1, 2, 3, 4, 5, 8, 13, 16, 17, 24, 31, 32, 33, 40)
-KINDS = ("plain", "scale", "glu", "residual", "out32", "col0", "blocks")
+KINDS = ("plain", "scale", "glu", "residual", "out32", "col0", "blocks", "topk")
 CASES = 200
 
 
@@ -53,6 +55,13 @@ def _case(i):
         c["blocks"] = [(str(r.choice(list(FMTS))), int(r.choice((32, 64, 96, 160, 256))), bool(r.integers(2)))
                        for _ in range(nb)]
         c["k"] = min(c["k"], 4352)
+    if kind == "topk":
+        c["m"] = min(c["m"], 32)
+        c["rows"] = int(r.integers(1, c["m"] + 1))
+        c["kk"] = int(r.choice([1, 2, 5, 8, 16, 32]))
+        c["cut"] = int(r.integers(0, 40)) if r.integers(2) else 0  # (valid columns: n - cut)
+        c["base"] = int(r.integers(0, 5000))
+        c["slots"] = int(r.choice([0, 3, 7]))  # (0: a record a tile; else tiles ranked in groups)
     if c["k"] >= 9216:
         c["n"] = min(c["n"], 256)  # (a split-K case: the oracle's float64 product stays small)
     return c
@@ -161,6 +170,23 @@ def test_sweep(device, i):
         check(f"{name} col0 {c0}", y[:, 32 * c0:32 * c0 + n], _ref64(x, h).float())
         rest = torch.cat([y[:, :32 * c0], y[:, 32 * c0 + n:]], 1)
         same(f"{name} col0 {c0}: the other columns untouched", rest, torch.full_like(rest, 7.0))
+    elif kind == "topk":
+        tw, h = _weight(device, n, k, fmt, 3000 + i)
+        rows, kk, base, slots = c["rows"], c["kk"], c["base"], c["slots"]
+        nv = max(1, n - c["cut"])
+        recs = linear.topk_slots(n, slots)
+        r = linear.topk_result(device, recs, rows, kk)
+        spec = {"r": r, "k": kk, "rows": rows, "slot0": 0, "base": base, "n": nv, "write_y": True, "slots": slots}
+        g = linear.launch_plan(tx, tw, None, topk=spec)["tiles_per_record"]
+        y = _host(linear.matmul(tx, tw, None, topk=spec), m, n)
+        check(f"{name} top-k: y", y, _ref64(x, h).float())
+        words = r.cpu().reshape(recs, -1)
+        want = O.tile_topk(y[:rows].numpy(), rows, kk, nv, base, width=32 * g)
+        same(f"{name} top-k rows {rows} k {kk} valid {nv} groups of {g}: records against the oracle's ranking of y",
+             words, torch.from_numpy(want.view(np.int32)))
+        r2 = linear.topk_result(device, recs, rows, kk)
+        linear.matmul(tx, tw, None, topk={**spec, "r": r2})
+        same(f"{name} top-k: repeated call", r2.cpu().reshape(recs, -1), words)
     else:  # blocks
         entries, wants, col, singles = [], [], 0, []
         for j, (bf, bn, scaled) in enumerate(c["blocks"]):

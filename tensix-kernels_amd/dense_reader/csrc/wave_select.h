@@ -221,7 +221,7 @@ __device__ __forceinline__ uint32_t wave_kth_largest(uint32_t m, int k) {
 #pragma unroll
     for (int b = 31; b >= 0; --b) {
         const uint32_t c = t | (1u << b);
-        if (__popcll(__ballot(m >= c)) >= k) t = c;
+        if ((int)__popcll(__ballot(m >= c)) >= k) t = c;
     }
     return t;
 }

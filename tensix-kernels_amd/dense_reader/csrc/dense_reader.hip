@@ -1900,6 +1900,11 @@ __device__ __forceinline__ void pair_tiles(const Args& a, const SegDev& sg, int 
     for (int q = 0; q < PW; ++q)
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) acc[q][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // the tiles' column scales, read before the K loop (after it, their round trip would end the workgroup)
+    __shared__ float psc[2][TILE];
+    float sc = 1.f;
+    const int su = (int)threadIdx.x >> 5, scol = (int)threadIdx.x & (TILE - 1);
+    if (su < nt && (t0 + su) * TILE + scol < sg.n_out) sc = load_scale(sg.scale, sg.scale_f32, (t0 + su) * TILE + scol);
     uint4* xs = reinterpret_cast<uint4*>(part) + wave * (XS_BYTES / 16);
     for (int ch = wave; ch < a.chunks; ch += a.waves) {
         const int k0 = ch * a.kch, k1 = min(k0 + a.kch, a.k_pad);
@@ -1917,9 +1922,10 @@ __device__ __forceinline__ void pair_tiles(const Args& a, const SegDev& sg, int 
             for (int j = 0; j < 4; ++j)
                 part[((((q >> 1) * W + wave) * 2 + (q & 1)) * ROWS + 16 * tt + 4 * (lane >> 4) + j) * 16 + (lane & 15)] =
                     acc[q][tt][j];
+    if (su < 2) psc[su][scol] = sc;
     __syncthreads();
     for (int u = 0; u < PW / 2 && u < nt; ++u)
-        epilogue<ROWS, 2>(a, sg, t0 + u, part + (size_t)u * W * 2 * ROWS * 16, W, tval, tkey, wave, lane);
+        epilogue<ROWS, 2>(a, sg, t0 + u, part + (size_t)u * W * 2 * ROWS * 16, W, tval, tkey, wave, lane, psc[u]);
 }
 
 template <int FMT, bool ONE>

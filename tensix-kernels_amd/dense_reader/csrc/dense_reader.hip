@@ -607,7 +607,8 @@ __device__ __forceinline__ float load_scale(const void* s, int f32, int col) {
 // under it instead of adding to the workgroup's end: thread c < TW (the tile's width) the scales of the tile's output
 // column c (gate and up with a GLU), thread e the residual of its first epilogue element (row e / TW, column e % TW).
 // After the K loop they go to LDS (pre: [0, TILE) the scale or gate scale, [TILE, 2 TILE) the up scale, from PRE_RES
-// the residual by thread), where the epilogue takes them.
+// the residual by thread), where the epilogue takes them. Only kernels of at most MAXW wavefronts stage into it (the
+// 16-wavefront MoE down kernels have no scales or residual and pass no pre).
 constexpr int PRE_RES = 2 * TILE;
 constexpr int PRE_FLOATS = PRE_RES + 64 * MAXW;
 

@@ -8,7 +8,7 @@ formats with per-block scales, and top-k records (bf16 keys, a record a tile or 
 from the oracle alone (oracle.held of the float weights, oracle.ref in float64, oracle.tile_topk's ranking of the op's
 own output), with the reference's bars (linear.py / test_dense_reader.py: 1 % relative Frobenius error and PCC 0.9999
 for bf16 outputs, 0.1 % for fp32 outputs, records bit for bit); every case is also called twice and must repeat bit
-for bit.
+for bit. A second sweep runs the top-k merge on seeded random records against the oracle's host merge.
 """
 
 import numpy as np
@@ -208,3 +208,42 @@ def test_sweep(device, i):
         for j, (c0, bn, _) in enumerate(wants):
             same(f"{name} block {j}: against one call per block", y[:, c0:c0 + bn],
                  one.float().cpu().reshape(m, -1)[:, c0:c0 + bn])
+
+
+MERGE_CASES = 60
+
+
+@pytest.mark.parametrize("i", range(MERGE_CASES))
+def test_merge_sweep(device, i):
+    """dr_topk_merge on seeded random records (record counts 1-9000, 1-32 rows, k 1-32, k_out 1-64, bf16 keys or fp32
+    scores; few distinct values, normal values or a ramp; slots unsorted or sorted within each record as the matmul
+    writes them) against the oracle's host merge, bit for bit."""
+    from test_dense_reader import _records
+
+    r = np.random.default_rng(9000 + i)
+    nrec = int(r.choice([1, 3, 17, 100, 517, 1024, 4008, 9000]))
+    rows = int(r.choice([1, 2, 3, 4, 7, 16, 32]))
+    k = int(r.choice([1, 2, 4, 5, 8, 16, 32]))
+    if rows * k > 256:
+        k = max(1, 256 // rows)
+    k_out = int(r.choice([1, 8, 16, 31, 32, 33, 64]))
+    fp32 = bool(r.integers(2))
+    kind = int(r.integers(3))
+    values = (np.array([-3.0, -1.0, 0.0, 0.5, 1.0, 2.0, 3.0], np.float32) if kind == 0 else
+              r.standard_normal(5000).astype(np.float32) if kind == 1 else np.arange(200, dtype=np.float32) / 7)
+    t = _records(nrec, rows, k, fp32, int(r.integers(1 << 30)), values)
+    name = f"merge sweep {i}: records {nrec} rows {rows} k {k} k_out {k_out} fp32 {fp32} values {kind}"
+    if r.integers(2):  # each record's slots sorted best first, as the matmul writes them
+        w = t.numpy().view(np.uint32).reshape(nrec, 2, rows, k).copy()
+        order = np.argsort(-w[:, 0].view(np.float32), axis=2, kind="stable") if fp32 else \
+            np.argsort(-w[:, 0].astype(np.int64), axis=2, kind="stable")
+        w[:, 0] = np.take_along_axis(w[:, 0], order, 2)
+        w[:, 1] = np.take_along_axis(w[:, 1], order, 2)
+        t = torch.from_numpy(w.reshape(nrec, -1).view(np.int32))
+        name += " sorted"
+    print(name, flush=True)
+    hv, hi = linear.records_host(t, rows, k, fp32=fp32)
+    wv, wi = O.global_topk(hv.numpy(), hi.numpy(), k_out)
+    gv, gi = linear.topk_merge(t.reshape(1, 1, nrec, -1).to(device.torch), rows, k, k_out=k_out, fp32=fp32)
+    same(f"{name}: values", gv.cpu(), torch.from_numpy(wv))
+    same(f"{name}: ids", gi.cpu().long(), torch.from_numpy(wi))

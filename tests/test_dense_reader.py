@@ -543,6 +543,33 @@ def test_split_k(device, fmt):
             same(f"{fmt} K {k} rows {m} block list second block", host(one, m, 640)[:, 384:], host(two, m, 640)[:, 384:])
 
 
+@pytest.mark.parametrize("fmt", ["bfp8", "bfp4", "bf16"])
+def test_long_k(device, fmt):
+    """K far past the configs' (a 70B-class FFN down's 28672, and 53280, ragged, split over seven workgroups a tile),
+    every kernel that serves it (GEMV 1-2 rows, MFMA 8 and 32 rows, 40 rows in two passes): against the oracle, repeated
+    calls bit-identical, a block list (up to 32 rows) bit-identical to one call per block."""
+    n = 96
+    for k in (28672, 53280):
+        wt = matrix(n, k, 95)
+        tw, _ = linear.native_weight(device, wt, DTYPES[fmt])
+        tb, _ = linear.native_weight(device, matrix(64, k, 96), DTYPES[fmt])
+        wk = held(tw, n)
+        for m in (1, 2, 8, 32, 40):
+            x, tx = x_input(device, m, k, 97 + m)
+            p = linear.launch_plan(tx, tw, None)
+            assert p["splits"] > 1, p
+            y = linear.matmul(tx, tw, None)
+            check(f"{fmt} K {k} rows {m} ({p['splits']} splits)", host(y, m, n), ref(x, wk))
+            same(f"{fmt} K {k} rows {m} repeated", host(linear.matmul(tx, tw, None), m, n), host(y, m, n))
+            if m > 32:
+                continue  # (a block list is a decode call: up to 32 rows)
+            one = linear.matmul(tx, [(tw, 0), (tb, 3)], None)
+            two = torch.zeros(1, 1, m, n + 64, dtype=torch.bfloat16, device=device.torch)
+            linear.matmul(tx, tw, None, out=two, col0=0)
+            linear.matmul(tx, tb, None, out=two, col0=3)
+            same(f"{fmt} K {k} rows {m} block list", host(one, m, n + 64), host(two, m, n + 64))
+
+
 def test_split_k_shapes_share_workspace(device):
     """Split-K launches of any shape share one workspace: many tiles after few (with counters placed by the tile count,
     the second launch's would lie where the first one's partial sums were), and back, each against the oracle."""

@@ -241,36 +241,38 @@ __device__ __forceinline__ void bfp8_step(float (&acc)[PW][MR], const float (&xs
 
 // bfp8: lane (kq, c) accumulates column c over k = 64 b + 16 kq + i; lane (kq, i) makes x' for that k. One chunk
 // [k0, k1) of one or two exponent groups (256 k each): x first, then the exponents, then the codes are issued (waits
-// are in issue order, so x' is made before the codes arrive); a one-group chunk loads its group twice (the second
-// copy is never used) so that no load sits under a branch.
-template <int MR, int PW>
+// are in issue order, so x' is made before the codes arrive). ONEG: every chunk of the launch is one group (256-k
+// chunks), and only that group is loaded; otherwise a one-group chunk (the last of a K that is an odd number of
+// groups) loads its group twice (the second copy is never used) so that no load sits under a branch.
+template <int MR, int PW, bool ONEG = false>
 __device__ __forceinline__ void chunk_bfp8(const Args& a, const uint8_t* const* cb, const uint8_t* const* eb, int k0,
                                            int k1, int lane, float (&acc)[PW][MR]) {
+    constexpr int NU = ONEG ? 4 : 8;  // 64-k blocks loaded
     const int g0 = k0 >> 8;
-    const bool two = k1 - k0 > 256;
+    const bool two = !ONEG && k1 - k0 > 256;
     const int g1 = two ? g0 + 1 : g0;
-    uint32_t xb[8][MR];
-    uint32_t e[2][PW];
-    Codes<PW> c[8];
+    uint32_t xb[NU][MR];
+    uint32_t e[NU / 4][PW];
+    Codes<PW> c[NU];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < NU; ++u) {
         const int b = 4 * (u < 4 ? g0 : g1) + (u & 3);
 #pragma unroll
         for (int m = 0; m < MR; ++m) xb[u][m] = x_bits(a, m, b * 64 + lane);
     }
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < NU / 4; ++h)
 #pragma unroll
         for (int q = 0; q < PW; ++q)
             e[h][q] = ld_stream4(eb[q] + (uint32_t)((h ? g1 : g0) * 256 + 4 * lane));
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < NU; ++u) {
         const int b = 4 * (u < 4 ? g0 : g1) + (u & 3);
 #pragma unroll
         for (int q = 0; q < PW; ++q) c[u].c[q] = ld_stream16(cb[q] + (uint32_t)(b * 1024 + lane * 16));
     }
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < NU; ++u) {
         if (u == 4 && !two) break;
         float xs[PW][MR];
 #pragma unroll
@@ -324,18 +326,19 @@ __device__ __forceinline__ int real_block(int b, int k) { return b * 128 >= k ? 
 // m) / 256 and sx (per lane, the x' it made) gives the (136 / 256) sum x' to take off; the caller scales the chunk's
 // difference by 256 (exact: the same value, rounded alike, as with the weights 136 + m, until those would overflow).
 // One chunk of one or two exponent groups (two blocks each), loaded as chunk_bfp8 loads its chunk.
-template <int MR, int PW>
+template <int MR, int PW, bool ONEG = false>
 __device__ __forceinline__ void chunk_bfp4(const Args& a, const uint8_t* const* cb, const uint8_t* const* eb, int k0,
                                            int k1, int lane, float (&acc)[PW][MR], float (&sx)[PW][MR]) {
+    constexpr int NU = ONEG ? 2 : 4;  // 128-k blocks loaded
     const int kq = lane >> 4, i = lane & 15;
     const int g0 = k0 >> 8;
-    const bool two = k1 - k0 > 256;
+    const bool two = !ONEG && k1 - k0 > 256;
     const int g1 = two ? g0 + 1 : g0;
-    uint32_t xp[4][MR];
-    uint32_t e[2][PW];
-    Codes<PW> c[4];
+    uint32_t xp[NU][MR];
+    uint32_t e[NU / 2][PW];
+    Codes<PW> c[NU];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < NU; ++u) {
         const int b = 2 * (u < 2 ? g0 : g1) + (u & 1);
         const int kp = b * 128 + kq * 32 + 2 * i;
         const int kc = min(kp, a.k - 2);  // (K is a multiple of 32: kp < K means kp + 1 < K)
@@ -347,18 +350,18 @@ __device__ __forceinline__ void chunk_bfp4(const Args& a, const uint8_t* const* 
         }
     }
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < NU / 2; ++h)
 #pragma unroll
         for (int q = 0; q < PW; ++q)
             e[h][q] = ld_stream4(eb[q] + (uint32_t)((h ? g1 : g0) * 256 + 4 * lane));
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < NU; ++u) {
         const int b = real_block(2 * (u < 2 ? g0 : g1) + (u & 1), a.k);
 #pragma unroll
         for (int q = 0; q < PW; ++q) c[u].c[q] = ld_stream16(cb[q] + (uint32_t)(b * 1024 + lane * 16));
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < NU; ++u) {
         if (u == 2 && !two) break;
         uint32_t xs[PW][MR];
 #pragma unroll
@@ -416,18 +419,19 @@ __device__ __forceinline__ void bfp4k_step(float (&t0)[PW][MR], float (&t1)[PW][
 // consecutive k of column c, two exponent groups of 16: its dot products over each group take x as it is (bf16 pairs,
 // broadcast across the row of 16 lanes) against the bf16 136 + m; less 136 times the group's x sum (the row's lanes
 // 0..7 or 8..15 hold its pairs), times 2^(E - 129) of the lane's group, added to the lane's sum: two FMAs a block.
-template <int MR, int PW>
+template <int MR, int PW, bool ONEG = false>
 __device__ __forceinline__ void chunk_bfp4k(const Args& a, const uint8_t* const* cb, const uint8_t* const* eb, int k0,
                                             int k1, int lane, float (&acc)[PW][MR]) {
+    constexpr int NU = ONEG ? 2 : 4;  // 128-k blocks loaded
     const int kq = lane >> 4, i = lane & 15;
     const int g0 = k0 >> 8;
-    const bool two = k1 - k0 > 256;
+    const bool two = !ONEG && k1 - k0 > 256;
     const int g1 = two ? g0 + 1 : g0;
-    uint32_t xp[4][MR];
-    uint32_t ex[4][PW];
-    Codes<PW> c[4];
+    uint32_t xp[NU][MR];
+    uint32_t ex[NU][PW];
+    Codes<PW> c[NU];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < NU; ++u) {
         const int b = 2 * (u < 2 ? g0 : g1) + (u & 1);
         const int kp = b * 128 + kq * 32 + 2 * i;
         const int kc = min(kp, a.k - 2);
@@ -439,20 +443,20 @@ __device__ __forceinline__ void chunk_bfp4k(const Args& a, const uint8_t* const*
         }
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < NU; ++u) {
         const int b = real_block(2 * (u < 2 ? g0 : g1) + (u & 1), a.k);
 #pragma unroll
         for (int q = 0; q < PW; ++q)
             ex[u][q] = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(eb[q] + (size_t)b * 128) + lane);
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < NU; ++u) {
         const int b = real_block(2 * (u < 2 ? g0 : g1) + (u & 1), a.k);
 #pragma unroll
         for (int q = 0; q < PW; ++q) c[u].c[q] = ld_stream16(cb[q] + (uint32_t)(b * 1024 + lane * 16));
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < NU; ++u) {
         if (u == 2 && !two) break;
         uint32_t xs[PW][MR];
         float rs0[MR], rs1[MR];  // 136 times the row's x sums over the two groups
@@ -492,18 +496,19 @@ __device__ __forceinline__ void chunk_bfp4k(const Args& a, const uint8_t* const*
 // k (int4/w4a16.py:1-19). Lane (kq, c)'s 32 k of a block are one scale group, so the lane's block sum is a group sum:
 // bf16 dot2 of x pairs (as they are) against 136 + q, less 136 times the row's x sum, times the lane's scale. Loads as
 // chunk_bfp4: x first, then the scales, then the codes.
-template <int MR, int PW>
+template <int MR, int PW, bool ONEG = false>
 __device__ __forceinline__ void chunk_int4(const Args& a, const uint8_t* const* cb, const uint16_t* const* gs, int k0,
                                            int k1, int lane, float (&acc)[PW][MR]) {
+    constexpr int NU = ONEG ? 2 : 4;  // 128-k blocks loaded
     const int kq = lane >> 4, i = lane & 15;
     const int g0 = k0 >> 8;
-    const bool two = k1 - k0 > 256;
+    const bool two = !ONEG && k1 - k0 > 256;
     const int g1 = two ? g0 + 1 : g0;
-    uint32_t xp[4][MR];
-    uint32_t sc[4][PW];
-    Codes<PW> c[4];
+    uint32_t xp[NU][MR];
+    uint32_t sc[NU][PW];
+    Codes<PW> c[NU];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < NU; ++u) {
         const int b = 2 * (u < 2 ? g0 : g1) + (u & 1);
         const int kp = b * 128 + kq * 32 + 2 * i;
         const int kc = min(kp, a.k - 2);
@@ -515,19 +520,19 @@ __device__ __forceinline__ void chunk_int4(const Args& a, const uint8_t* const* 
         }
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < NU; ++u) {
         const int b = 2 * (u < 2 ? g0 : g1) + (u & 1);
 #pragma unroll
         for (int q = 0; q < PW; ++q) sc[u][q] = __builtin_nontemporal_load(gs[q] + (size_t)b * 64 + lane);
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < NU; ++u) {
         const int b = 2 * (u < 2 ? g0 : g1) + (u & 1);
 #pragma unroll
         for (int q = 0; q < PW; ++q) c[u].c[q] = ld_stream16(cb[q] + (uint32_t)(b * 1024 + lane * 16));
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < NU; ++u) {
         if (u == 2 && !two) break;
         uint32_t xs[PW][MR];
         float rs[MR];  // the row's x sum (the 16 lanes' pairs): 136 times it is in every dot of the row
@@ -1086,8 +1091,11 @@ __device__ __forceinline__ constexpr bool moe_n() {
     return MOE == DR_MOE_GATE_UP || MOE == DR_MOE_GATE_UP_ROWS;
 }
 
-template <int MR, int PW, int FMT, bool ONE>
-__global__ __launch_bounds__(512) void dr_gemv(const Args a) {
+// ONEG: the launch's chunks are 256 k, one exponent group each, and the loaders read only that group (the dense
+// kernel keeps its own instantiation: a runtime choice of loader inside it moved the compiler's scheduling of its K
+// loop, NS 12.5 -> 13.1 us)
+template <int MR, int PW, int FMT, bool ONE, bool ONEG>
+__device__ __forceinline__ void gemv_body(const Args a) {
     extern __shared__ float part[];  // [W][PW][MR][16]
     __shared__ float tval[MR][TILE];
     __shared__ __align__(16) uint32_t tkey[MR][TILE];
@@ -1120,19 +1128,19 @@ __global__ __launch_bounds__(512) void dr_gemv(const Args a) {
             for (int m = 0; m < MR; ++m) acc[q][m] = corr[q][m] = 0.f;
         const int k0 = ch * a.kch, k1 = min(k0 + a.kch, a.k_pad);
         if (fmt == DR_BFP8) {
-            chunk_bfp8<MR, PW>(a, cb, eb, k0, k1, lane, acc);
+            chunk_bfp8<MR, PW, ONEG>(a, cb, eb, k0, k1, lane, acc);
         } else if (FMT == DR_INT4) {
             const uint16_t* gs[PW];
 #pragma unroll
             for (int q = 0; q < PW; ++q) gs[q] = sg.gscale + (size_t)(PW * t + q) * (a.k_pad / 128) * 64;
-            chunk_int4<MR, PW>(a, cb, gs, k0, k1, lane, acc);
+            chunk_int4<MR, PW, ONEG>(a, cb, gs, k0, k1, lane, acc);
         } else if (fmt == DR_BFP4) {
             float sx[PW][MR];
 #pragma unroll
             for (int q = 0; q < PW; ++q)
 #pragma unroll
                 for (int m = 0; m < MR; ++m) sx[q][m] = 0.f;
-            chunk_bfp4<MR, PW>(a, cb, eb, k0, k1, lane, acc, sx);
+            chunk_bfp4<MR, PW, ONEG>(a, cb, eb, k0, k1, lane, acc, sx);
             // the wavefront's sum of x' (every lane made distinct x'): its excess is taken off every column
 #pragma unroll
             for (int q = 0; q < PW; ++q)
@@ -1164,6 +1172,17 @@ __global__ __launch_bounds__(512) void dr_gemv(const Args a) {
     __syncthreads();
     const int nparts = gather_splits<MR, PW>(a, g, split, part);
     if (nparts) epilogue<MR, PW>(a, sg, t, part, nparts, tval, tkey, wave, lane, pre);
+}
+
+template <int MR, int PW, int FMT, bool ONE>
+__global__ __launch_bounds__(512) void dr_gemv(const Args a) {
+    gemv_body<MR, PW, FMT, ONE, false>(a);
+}
+
+// the same for launches of 256-k chunks (K up to 2048)
+template <int MR, int PW, int FMT, bool ONE>
+__global__ __launch_bounds__(512) void dr_gemv_g1(const Args a) {
+    gemv_body<MR, PW, FMT, ONE, true>(a);
 }
 
 
@@ -2346,8 +2365,8 @@ bool narrow_better(int tiles) {
     return (2 * tiles + c - 1) / c < 2 * ((tiles + c - 1) / c);
 }
 
-// the K range of one chunk: 512 (two exponent groups) from K = 2048 up, else 256 (at least four chunks, so four
-// wavefronts a tile)
+// the K range of one chunk: 512 (two exponent groups) past K = 2048, else 256 (K = 2048: eight wavefronts of one group
+// each, rather than four of two: the bfloat8_b GEMV at N = 4096 4.30 -> 4.09 us)
 #ifndef DR_CHUNK_K
 #define DR_CHUNK_K 0
 #endif
@@ -2370,7 +2389,7 @@ void plan_chunks(int k_pad, int ch, int* chunks, int* kch, int* waves, int* spli
 
 void plan(int k, int* chunks, int* kch, int* waves, int* splits, int* cps) {
     const int k_pad = (k + KALIGN - 1) / KALIGN * KALIGN;
-    plan_chunks(k_pad, DR_CHUNK_K ? DR_CHUNK_K : (k_pad >= 2048 ? 512 : 256), chunks, kch, waves, splits, cps);
+    plan_chunks(k_pad, DR_CHUNK_K ? DR_CHUNK_K : (k_pad > 2048 ? 512 : 256), chunks, kch, waves, splits, cps);
 }
 
 // a launch of more tiles than the workspace has counters for runs unsplit
@@ -2402,17 +2421,38 @@ template <int MR, int PW>
 void launch_gemv(const Args& a, int grid, hipStream_t st) {
     const dim3 b(64 * a.waves);
     const size_t lds = dense_lds(a, PW, MR);
+    const bool g1 = a.kch == 256;
     if (a.nseg > 1) {
-        hipLaunchKernelGGL((dr_gemv<MR, PW, -1, false>), dim3(grid), b, lds, st, a);
+        if (g1)
+            hipLaunchKernelGGL((dr_gemv_g1<MR, PW, -1, false>), dim3(grid), b, lds, st, a);
+        else
+            hipLaunchKernelGGL((dr_gemv<MR, PW, -1, false>), dim3(grid), b, lds, st, a);
         return;
     }
     switch (a.seg[0].fmt) {
-        case DR_BFP8: hipLaunchKernelGGL((dr_gemv<MR, PW, DR_BFP8, true>), dim3(grid), b, lds, st, a); break;
-        case DR_BFP4: hipLaunchKernelGGL((dr_gemv<MR, PW, DR_BFP4, true>), dim3(grid), b, lds, st, a); break;
-        case DR_INT4:
-            if constexpr (PW <= 2 && MR <= 2) hipLaunchKernelGGL((dr_gemv<MR, PW, DR_INT4, true>), dim3(grid), b, lds, st, a);
+        case DR_BFP8:
+            if (g1)
+                hipLaunchKernelGGL((dr_gemv_g1<MR, PW, DR_BFP8, true>), dim3(grid), b, lds, st, a);
+            else
+                hipLaunchKernelGGL((dr_gemv<MR, PW, DR_BFP8, true>), dim3(grid), b, lds, st, a);
             break;
-        default: hipLaunchKernelGGL((dr_gemv<MR, PW, DR_BF16, true>), dim3(grid), b, lds, st, a); break;
+        case DR_BFP4:
+            if (g1)
+                hipLaunchKernelGGL((dr_gemv_g1<MR, PW, DR_BFP4, true>), dim3(grid), b, lds, st, a);
+            else
+                hipLaunchKernelGGL((dr_gemv<MR, PW, DR_BFP4, true>), dim3(grid), b, lds, st, a);
+            break;
+        case DR_INT4:
+            if constexpr (PW <= 2 && MR <= 2) {
+                if (g1)
+                    hipLaunchKernelGGL((dr_gemv_g1<MR, PW, DR_INT4, true>), dim3(grid), b, lds, st, a);
+                else
+                    hipLaunchKernelGGL((dr_gemv<MR, PW, DR_INT4, true>), dim3(grid), b, lds, st, a);
+            }
+            break;
+        default:  // (bf16 chunks have no exponent groups: one kernel serves every chunk size)
+            hipLaunchKernelGGL((dr_gemv<MR, PW, DR_BF16, true>), dim3(grid), b, lds, st, a);
+            break;
     }
 }
 

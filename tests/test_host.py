@@ -83,7 +83,7 @@ def test_plan_depends_on_k_only():
     for k in (32, 1024, 2048, 4096, 14336):
         c, kch, _ = _lib.plan(k, 1)
         k_pad = -(-k // 256) * 256
-        assert kch == (512 if k_pad >= 2048 else 256) and c == -(-k_pad // kch)
+        assert kch == (512 if k_pad > 2048 else 256) and c == -(-k_pad // kch)
         for m in (2, 8, 32):
             assert _lib.plan(k, m)[:2] == (c, kch)
     assert [_lib.plan(4096, m)[2] for m in (1, 2, 3, 16, 17, 32, 100)] == [1, 2, 16, 16, 32, 32, 32]

@@ -14,9 +14,9 @@
 // exponents per 256 k. K is padded to 256 and N to 32 (or what the caller asks); padding holds zeros (m = 0).
 //
 // The matmul (dr_gemv) gives each 32-column output tile one workgroup. K is cut into chunks of 256 or 512 values (by
-// K alone); a wavefront sums the tile's panels over one chunk at a time, with every load of the chunk in flight at
-// once, and the chunks' partial sums are added in chunk order. The split depends on K only, so every weight of one K
-// sees the same sums in the same order: a block list equals one call per block bit for bit,
+// K and the kernel); a wavefront sums the tile's panels over one chunk at a time, with every load of the chunk in
+// flight at once, and the chunks' partial sums are added in chunk order. The split depends on K and the kernel only,
+// so every weight of one K sees the same sums in the same order: a block list equals one call per block bit for bit,
 // and repeated calls are bit-identical. Decode stays in registers: the block-float exponent of (k, panel) is folded
 // into x once per (k, panel) -- x * 2^(E - bias) is exact -- and broadcast across the 16 lanes of a row with DPP
 // row_newbcast, so each weight value costs one convert and one FMA (bfp8), or, for bfp4, half a byte permute and half
@@ -2366,7 +2366,11 @@ bool narrow_better(int tiles) {
 }
 
 // the K range of one chunk: 512 (two exponent groups) past K = 2048, else 256 (K = 2048: eight wavefronts of one group
-// each, rather than four of two: the bfloat8_b GEMV at N = 4096 4.30 -> 4.09 us)
+// each, rather than four of two: the bfloat8_b GEMV at N = 4096 4.30 -> 4.09 us). The MFMA kernel (16 or 32 rows a
+// pass), which walks a chunk's groups one after another, takes 256 up to K = 3072 too, so that a tile has eight
+// wavefronts rather than six or fewer (K = 2304 and 3072 at 3-32 rows 2-22 % faster; at K = 3584, seven chunks of 512
+// against eight wavefronts with two of 256 for most, 16 rows lost 4-6 %; the GEMV at K = 3072 gains at N = 4096 and
+// loses at N = 8192).
 #ifndef DR_CHUNK_K
 #define DR_CHUNK_K 0
 #endif
@@ -2387,9 +2391,10 @@ void plan_chunks(int k_pad, int ch, int* chunks, int* kch, int* waves, int* spli
     *waves = *cps < MAXW ? *cps : MAXW;
 }
 
-void plan(int k, int* chunks, int* kch, int* waves, int* splits, int* cps) {
+void plan(int k, bool mfma, int* chunks, int* kch, int* waves, int* splits, int* cps) {
     const int k_pad = (k + KALIGN - 1) / KALIGN * KALIGN;
-    plan_chunks(k_pad, DR_CHUNK_K ? DR_CHUNK_K : (k_pad > 2048 ? 512 : 256), chunks, kch, waves, splits, cps);
+    const int ch = DR_CHUNK_K ? DR_CHUNK_K : (k_pad > (mfma ? 3072 : 2048) ? 512 : 256);
+    plan_chunks(k_pad, ch, chunks, kch, waves, splits, cps);
 }
 
 // a launch of more tiles than the workspace has counters for runs unsplit
@@ -2640,7 +2645,7 @@ int dr_unpack(const void* codes, const void* exps, int fmt, int n, int k, int n_
 int dr_plan(int k, int m, int32_t* chunks, int32_t* kch, int32_t* rpp) {
     if (k <= 0 || m <= 0) return DR_EINVAL;
     int c, ch, w, sp, cps;
-    plan(k, &c, &ch, &w, &sp, &cps);
+    plan(k, rows_per_pass(m) >= 16, &c, &ch, &w, &sp, &cps);
     if (chunks) *chunks = c;
     if (kch) *kch = ch;
     if (rpp) *rpp = rows_per_pass(m);
@@ -2744,13 +2749,13 @@ int prepare(const dr_launch* L, Args& a, int& pw, int& tiles, int& mr, bool gath
         a.write_y = T.write_y != 0;
         a.tk_fp32 = T.fp32 != 0;
     }
-    plan(L->k, &a.chunks, &a.kch, &a.waves, &a.splits, &a.cps);
-    a.tiles = tiles;
-    limit_splits(a);
     mr = rows_per_pass(L->m);
     if (pw == 4 && mr == 8) mr = 4;    // (GLU: at most 4 GEMV rows or 16 MFMA rows a pass, for the registers
     if (pw == 4 && mr == 32) mr = 16;  // and the LDS)
     if (a.seg[0].fmt == DR_INT4) mr = L->m >= 2 ? 2 : 1;  // (int4: the GEMV, two rows a pass)
+    plan(L->k, !gather && mr >= 16, &a.chunks, &a.kch, &a.waves, &a.splits, &a.cps);  // (the expert gather: as before)
+    a.tiles = tiles;
+    limit_splits(a);
     // A GEMV launch takes 16-column tiles (one panel a workgroup) where they lower the most any CU streams (fewer
     // 32-column tiles than CUs, or a count just past a multiple of the CUs): each column's sums are made by the same
     // lanes in the same order whatever the tile width, so the results are the same bit for bit. (Not with top-k
@@ -2764,7 +2769,7 @@ int prepare(const dr_launch* L, Args& a, int& pw, int& tiles, int& mr, bool gath
             tiles += a.seg[i].tiles;
         }
         a.tiles = tiles;
-        plan(L->k, &a.chunks, &a.kch, &a.waves, &a.splits, &a.cps);
+        plan(L->k, false, &a.chunks, &a.kch, &a.waves, &a.splits, &a.cps);
         limit_splits(a);
     }
     // 32 rows, plain tiles, more tiles than CUs: block-float segments in tile pairs (dr_mfma_pairs)

@@ -256,8 +256,9 @@ def choose(device, x, w, full_sync=False, **forced):
 
 class BlockListMismatch(ValueError):
     """A block list refused before its launch because its output would not equal one call per block bit for bit
-    (reference linear.py:498-501). The MI355X split depends on K alone, which a block list's weights share, so the
-    output always equals one call per block; the class is kept for callers that catch it."""
+    (reference linear.py:498-501). The MI355X split depends on K and the rows (which kernel runs) alone, which a block
+    list's weights share, so the output always equals one call per block; the class is kept for callers that catch
+    it."""
 
 
 def is_block_list(w):

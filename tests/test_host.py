@@ -77,15 +77,18 @@ def test_struct_layout_matches_c(tmp_path):
     assert got == want
 
 
-def test_plan_depends_on_k_only():
+def test_plan_depends_on_k_and_kernel():
+    """The chunking is a function of K and the kernel (the GEMV for 1-2 rows, the MFMA kernel from 3): 512-k chunks past
+    K = 2048 on the GEMV, past K = 3072 on the MFMA kernel, else 256."""
     lib = _lib.lib()
     assert lib.dr_version() >= 1
-    for k in (32, 1024, 2048, 4096, 14336):
-        c, kch, _ = _lib.plan(k, 1)
+    for k in (32, 1024, 2048, 2080, 3072, 3584, 4096, 14336):
         k_pad = -(-k // 256) * 256
-        assert kch == (512 if k_pad > 2048 else 256) and c == -(-k_pad // kch)
-        for m in (2, 8, 32):
-            assert _lib.plan(k, m)[:2] == (c, kch)
+        for ms, last in (((1, 2), 2048), ((3, 8, 16, 17, 32, 100), 3072)):
+            c, kch, _ = _lib.plan(k, ms[0])
+            assert kch == (512 if k_pad > last else 256) and c == -(-k_pad // kch), (k, ms, kch)
+            for m in ms[1:]:
+                assert _lib.plan(k, m)[:2] == (c, kch), (k, m)
     assert [_lib.plan(4096, m)[2] for m in (1, 2, 3, 16, 17, 32, 100)] == [1, 2, 16, 16, 32, 32, 32]
 
 

@@ -175,7 +175,9 @@ int dr_topk_merge(const void* records, int n_records, int rows, int k, int fp32,
                   int32_t* ids, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* The work split for K and M: chunks (waves per output tile, each a K range of kch values) and the rows a pass
- * takes. For inspection; results depend only on what this returns. */
+ * takes (M picks the kernel: the GEMV for 1-2 rows, the MFMA kernel from 3, whose chunks are 256 k up to K = 3072
+ * against the GEMV's up to 2048). For inspection of block-float and bf16 weights (an int4 weight runs the GEMV at any
+ * M; dr_launch_plan gives any launch's own plan); results depend only on what this returns. */
 int dr_plan(int k, int m, int32_t* chunks, int32_t* kch, int32_t* rows_per_pass);
 
 /* What dr_matmul would launch for this launch, for inspection (replaces the plan dict that dense_reader/linear.py:

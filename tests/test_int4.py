@@ -67,10 +67,12 @@ def test_matmul(device, fid):
              host(w4a16.w4a16_linear(tx, wq, ts, split=False, cores_per_bank=2, fidelity=fid), n), y)
 
 
-def test_rows(device):
+@pytest.mark.parametrize("k", [2048, 4096])
+def test_rows(device, k):
     """Several rows through the C ABI (two a pass, the last pass partial): each row against the oracle and against the
-    one-token call on that row, bit for bit (the rows of a pass are summed in the same order as a lone row)."""
-    k, n = 4096, 1056
+    one-token call on that row, bit for bit (the rows of a pass are summed in the same order as a lone row); at K = 2048
+    the launches take 256-k chunks, at 4096 512-k chunks."""
+    n = 1056
     codes, scales = make_case(n, k, 21)
     wq = w4a16.int4_weight(device, codes)
     ts = w4a16.group_scales(device, scales)

@@ -2514,8 +2514,10 @@ hipError_t launch_moe(const MoeArgs& a, int mode, int rows, int pw, int grid, hi
             else if (rows == 2)
                 narrow ? launch_gemv_moe<2, 2, DR_MOE_GATE_UP_ROWS>(a, grid, st)
                        : launch_gemv_moe<2, 4, DR_MOE_GATE_UP_ROWS>(a, grid, st);
-            else
+            else if (rows == 16)
                 launch_mfma_moe<1, 4, DR_MOE_GATE_UP_ROWS>(a, grid, st);
+            else
+                launch_mfma_moe<2, 4, DR_MOE_GATE_UP_ROWS>(a, grid, st);
             break;
         default:
             if (rows == 1)
@@ -3038,7 +3040,10 @@ int prepare_moe(const dr_launch* L, const dr_moe* M, MoeArgs& a, int& pw, int& t
     else if (L->m <= 2)
         mr = L->m;
     else
-        mr = (nmode || L->m <= 16) ? 16 : 32;
+        // (gate/up: one 32-row pass for 17-24 rows rather than two of 16, whose second streams every weight again for
+        // a few rows: 17, 20 and 24 rows 155, 169, 177 -> 127, 148, 161 us at the gpt-oss shape; from 26 rows two
+        // passes of 16 are as fast or faster, the 32-row tiles reading 32 rows of x each)
+        mr = (L->m <= 16 || (nmode && L->m > 24)) ? 16 : 32;
     if (nmode) {
         // the MFMA rows of gate/up: 256-k chunks up to K = 3072, as the dense MFMA kernel's (the gpt-oss gate/up at 3,
         // 8, 16 and 32 rows 44.2, 80.3, 93.9, 225 -> 32.6, 69.8, 79.0, 188 us)

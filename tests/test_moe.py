@@ -341,6 +341,8 @@ def test_rows(device):
     rows_case(device, gu, dn, P, 32, act="gelu_tanh", seed=3)
     rows_case(device, gu, dn, P, 5, seed=2, ids32=True)
     rows_case(device, gu, dn, P, 17, seed=8)
+    rows_case(device, gu, dn, P, 24, seed=9)  # (gate_up: the last rows of one 32-row pass)
+    rows_case(device, gu, dn, P, 25, seed=10)  # (gate_up: two passes of 16 rows again)
 
 
 def test_rows_one_row_equals_decode(device):

@@ -298,6 +298,29 @@ def test_rows32_staged_x(device, fmt):
             same(f"{fmt} K {k} rows {m}: rows permuted", yp, y[perm])
 
 
+@pytest.mark.parametrize("fmt", ["bfp8", "bfp4", "bf16"])
+def test_rows_in_passes_bitwise(device, fmt):
+    """Past 32 rows the launch runs passes of 32 (a last pass of at most 16 rows on the 16-row kernel): each pass's rows
+    equal bit for bit those of a call on those rows alone, and the 16- and 32-row kernels sum a row alike. At 300 tiles
+    (the 32-row passes take tile pairs) and at a K split over workgroups."""
+    for k, n in ((1024, 9600), (9216, 320)):
+        wt = matrix(n, k, 130)
+        tw, _ = linear.native_weight(device, wt, DTYPES[fmt])
+        wk = held(tw, n)
+        for m in (40, 45, 70):
+            x, tx = x_input(device, m, k, 131 + m)
+            y = host(linear.matmul(tx, tw, None), m, n)
+            check(f"{fmt} K {k} N {n} rows {m}", y, ref(x, wk))
+            for r0 in range(0, m, 32):
+                r1 = min(r0 + 32, m)
+                one = host(linear.matmul(tx[..., r0:r1, :].contiguous(), tw, None), r1 - r0, n)
+                same(f"{fmt} K {k} N {n} rows {m}: rows {r0}-{r1 - 1} against a call on them alone", y[r0:r1], one)
+        x, tx = x_input(device, 32, k, 140)
+        y32 = host(linear.matmul(tx, tw, None), 32, n)
+        y16 = torch.cat([host(linear.matmul(tx[..., r:r + 16, :].contiguous(), tw, None), 16, n) for r in (0, 16)])
+        same(f"{fmt} K {k} N {n}: 32 rows against two calls of 16", y32, y16)
+
+
 def test_rows32_tile_pairs(device):
     """A 32-row launch of more tiles than CUs runs its block-float segments' tiles in pairs, a workgroup each (the
     last of an odd count alone), and its bf16 segments' one a workgroup: a block list of bfloat8_b (129 tiles, odd),

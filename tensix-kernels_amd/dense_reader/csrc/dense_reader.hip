@@ -2028,6 +2028,10 @@ __global__ __launch_bounds__(512) void dr_mfma_moe(const MoeArgs a) {
     // memory: one dependent round trip fewer a chunk)
     int idv = -1;
     if constexpr (MOE == DR_MOE_DOWN) idv = lane < a.slots ? moe_id(a, 0, lane) : -1;
+    // gate/up rows at 32 rows: x through each wavefront's LDS staging, as the dense 32-row kernel reads it (the same
+    // sums; x read in whole lines)
+    constexpr bool XLG = MOE == DR_MOE_GATE_UP_ROWS && MT == 2 && !KB;
+    uint4* xs = reinterpret_cast<uint4*>(part) + wave * (XS_BYTES / 16);
     const int ch1 = min((split + 1) * a.cps, a.chunks);
     for (int ch = split * a.cps + wave; ch < ch1; ch += a.waves) {
         const int k0 = ch * a.kch, k1 = min(k0 + a.kch, a.k_pad);
@@ -2049,9 +2053,13 @@ __global__ __launch_bounds__(512) void dr_mfma_moe(const MoeArgs a) {
             }
             chunk(b, cbe, ebe, k0 - s * a.ekp, k1 - s * a.ekp);
         } else {
-            chunk(a, cb, eb, k0, k1);
+            if constexpr (XLG)
+                xl_chunk_bfp4<PW>(a, cb, eb, k0, k1, lane, acc, xs);
+            else
+                chunk(a, cb, eb, k0, k1);
         }
     }
+    if constexpr (XLG) __syncthreads();  // (every wavefront done with its staging before any partial lands on it)
 #pragma unroll
     for (int q = 0; q < PW; ++q)
 #pragma unroll
@@ -2489,7 +2497,8 @@ void launch_gemv_moe(const MoeArgs& a, int grid, hipStream_t st) {
 template <int MT, int PW, int MOE>
 void launch_mfma_moe(const MoeArgs& a, int grid, hipStream_t st) {
     const dim3 b(64 * a.waves);
-    const size_t lds = (size_t)max(a.waves, a.splits) * PW * 16 * MT * 16 * sizeof(float);
+    size_t lds = (size_t)max(a.waves, a.splits) * PW * 16 * MT * 16 * sizeof(float);
+    if (MOE == DR_MOE_GATE_UP_ROWS && MT == 2) lds = max(lds, (size_t)a.waves * XS_BYTES);  // (the x staging)
     if (a.seg[0].fmt == DR_BFP4_KB)
         hipLaunchKernelGGL((dr_mfma_moe<MT, PW, MOE, true>), dim3(grid), b, lds, st, a);
     else
@@ -3043,10 +3052,9 @@ int prepare_moe(const dr_launch* L, const dr_moe* M, MoeArgs& a, int& pw, int& t
     else if (L->m <= 2)
         mr = L->m;
     else
-        // (gate/up: one 32-row pass for 17-24 rows rather than two of 16, whose second streams every weight again for
-        // a few rows: 17, 20 and 24 rows 155, 169, 177 -> 127, 148, 161 us at the gpt-oss shape; from 26 rows two
-        // passes of 16 are as fast or faster, the 32-row tiles reading 32 rows of x each)
-        mr = (L->m <= 16 || (nmode && L->m > 24)) ? 16 : 32;
+        // (gate/up too: one 32-row pass, x staged through LDS, rather than two of 16, whose second streams every
+        // weight again: 17, 24 and 32 rows 155, 177, 188 -> 121, 134, 149 us at the gpt-oss shape)
+        mr = L->m <= 16 ? 16 : 32;
     if (nmode) {
         // the MFMA rows of gate/up: 256-k chunks up to K = 3072, as the dense MFMA kernel's (the gpt-oss gate/up at 3,
         // 8, 16 and 32 rows 44.2, 80.3, 93.9, 225 -> 32.6, 69.8, 79.0, 188 us)

@@ -1402,9 +1402,11 @@ struct XStage {
     __amdgpu_buffer_rsrc_t r;
     uint32_t off[4];  // the lane's byte offset for loads i with (i & 3) == j (16 chunks) or (i & 1) == j (8)
     uint32_t ldx2;
-    __device__ __forceinline__ XStage(const Args& a, int lane) {
+    // xbytes: the bytes from a.x on that the loads may read (0: m rows of ldx)
+    __device__ __forceinline__ XStage(const Args& a, int lane, uint32_t xbytes = 0) {
         ldx2 = 2u * (uint32_t)a.ldx;
-        r = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)(ldx2 * (uint32_t)a.m), 0x00020000);
+        r = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)(xbytes ? xbytes : ldx2 * (uint32_t)a.m),
+                                              0x00020000);
         const int l = (int)opaque((uint32_t)lane);  // (made per chunk, not held across the kernel's chunk loop)
         const int row = l / NCH, c0 = (l % NCH) ^ x_swz<NCH>(row);
 #pragma unroll
@@ -1752,9 +1754,9 @@ __device__ __forceinline__ void xl_chunk_bfp8(const Args& a, const uint8_t* cons
 // bfloat4_b: a step is block k / 128; MFMA D takes k = 32 kq + 8 D + j of the step
 template <int PW>
 __device__ __forceinline__ void xl_chunk_bfp4(const Args& a, const uint8_t* const* cb, const uint8_t* const* eb, int k0,
-                                              int k1, int lane, f32x4 (&acc)[PW][2], uint4* xs) {
+                                              int k1, int lane, f32x4 (&acc)[PW][2], uint4* xs, uint32_t xbytes = 0) {
     const int ns = (k1 - k0) >> 7;
-    const XStage<16> xst(a, lane);
+    const XStage<16> xst(a, lane, xbytes);
     uint4 cn[PW];
     uint32_t en[PW], e[PW];
     auto issue = [&](int s) {
@@ -2028,9 +2030,10 @@ __global__ __launch_bounds__(512) void dr_mfma_moe(const MoeArgs a) {
     // memory: one dependent round trip fewer a chunk)
     int idv = -1;
     if constexpr (MOE == DR_MOE_DOWN) idv = lane < a.slots ? moe_id(a, 0, lane) : -1;
-    // gate/up rows at 32 rows: x through each wavefront's LDS staging, as the dense 32-row kernel reads it (the same
-    // sums; x read in whole lines)
+    // 32 rows: x through each wavefront's LDS staging, as the dense 32-row kernel reads it (the same sums; x read in
+    // whole lines). The down's chunk views x from its unit's block on, so its staging may read only up to x's end.
     constexpr bool XLG = MOE == DR_MOE_GATE_UP_ROWS && MT == 2 && !KB;
+    constexpr bool XLD = MOE == DR_MOE_DOWN_ROWS && MT == 2 && !KB;
     uint4* xs = reinterpret_cast<uint4*>(part) + wave * (XS_BYTES / 16);
     const int ch1 = min((split + 1) * a.cps, a.chunks);
     for (int ch = split * a.cps + wave; ch < ch1; ch += a.waves) {
@@ -2051,7 +2054,12 @@ __global__ __launch_bounds__(512) void dr_mfma_moe(const MoeArgs a) {
                 cbe[q] = cb[q] + (size_t)e * a.cstride;
                 ebe[q] = eb[q] + (size_t)e * a.estride;
             }
-            chunk(b, cbe, ebe, k0 - s * a.ekp, k1 - s * a.ekp);
+            if constexpr (XLD) {
+                const uint32_t xb = 2u * (uint32_t)a.ldx * (uint32_t)a.m - 2u * (uint32_t)(s * a.ek);  // (to x's end)
+                xl_chunk_bfp4<PW>(b, cbe, ebe, k0 - s * a.ekp, k1 - s * a.ekp, lane, acc, xs, xb);
+            } else {
+                chunk(b, cbe, ebe, k0 - s * a.ekp, k1 - s * a.ekp);
+            }
         } else {
             if constexpr (XLG)
                 xl_chunk_bfp4<PW>(a, cb, eb, k0, k1, lane, acc, xs);
@@ -2059,7 +2067,7 @@ __global__ __launch_bounds__(512) void dr_mfma_moe(const MoeArgs a) {
                 chunk(a, cb, eb, k0, k1);
         }
     }
-    if constexpr (XLG) __syncthreads();  // (every wavefront done with its staging before any partial lands on it)
+    if constexpr (XLG || XLD) __syncthreads();  // (every wavefront done with its staging before any partial lands on it)
 #pragma unroll
     for (int q = 0; q < PW; ++q)
 #pragma unroll
@@ -2498,7 +2506,8 @@ template <int MT, int PW, int MOE>
 void launch_mfma_moe(const MoeArgs& a, int grid, hipStream_t st) {
     const dim3 b(64 * a.waves);
     size_t lds = (size_t)max(a.waves, a.splits) * PW * 16 * MT * 16 * sizeof(float);
-    if (MOE == DR_MOE_GATE_UP_ROWS && MT == 2) lds = max(lds, (size_t)a.waves * XS_BYTES);  // (the x staging)
+    if ((MOE == DR_MOE_GATE_UP_ROWS || MOE == DR_MOE_DOWN_ROWS) && MT == 2)
+        lds = max(lds, (size_t)a.waves * XS_BYTES);  // (the x staging)
     if (a.seg[0].fmt == DR_BFP4_KB)
         hipLaunchKernelGGL((dr_mfma_moe<MT, PW, MOE, true>), dim3(grid), b, lds, st, a);
     else

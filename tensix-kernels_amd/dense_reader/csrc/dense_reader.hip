@@ -2084,6 +2084,68 @@ __global__ __launch_bounds__(512) void dr_mfma_moe(const MoeArgs a) {
         epilogue<ROWS, PW>(a, sg, t, part, nparts, tval, tkey, wave, lane);
 }
 
+// DR_MOE_GATE_UP_ROWS at 32 rows: two adjacent 32-column tiles of one unit's expert a workgroup, so the wavefronts'
+// staged x serves both (the unit's tiles in pairs, the last of an odd count alone): the gpt-oss gate/up at 17, 24 and
+// 32 rows 122, 135, 148 -> 107, 125, 128 us. Each tile's panels are summed by the same lanes, steps and wavefronts in
+// the same order as in dr_mfma_moe<2, 4> (xl_chunk_bfp4 over more panels), so the results do not change.
+template <int NT>
+__device__ __forceinline__ void moe_pair_tiles(const MoeArgs& a, int t0, int unit, int ex, int wave, int lane,
+                                               float* part) {
+    constexpr int PW = 4 * NT, ROWS = 32;
+    const SegDev& sg = a.seg[0];
+    const uint8_t* cb[PW];
+    const uint8_t* eb[PW];
+#pragma unroll
+    for (int u = 0; u < NT; ++u) {
+        const uint8_t* c4[4];
+        const uint8_t* e4[4];
+        panel_ptrs<4>(sg, t0 + u, a.k_pad, c4, e4);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            cb[4 * u + q] = c4[q] + (size_t)ex * a.cstride;
+            eb[4 * u + q] = e4[q] + (size_t)ex * a.estride;
+        }
+    }
+    f32x4 acc[PW][2];
+#pragma unroll
+    for (int q = 0; q < PW; ++q)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) acc[q][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    uint4* xs = reinterpret_cast<uint4*>(part) + wave * (XS_BYTES / 16);
+    for (int ch = wave; ch < a.chunks; ch += a.waves) {
+        const int k0 = ch * a.kch, k1 = min(k0 + a.kch, a.k_pad);
+        xl_chunk_bfp4<PW>(a, cb, eb, k0, k1, lane, acc, xs);
+    }
+#pragma unroll
+    for (int u = 0; u < NT; ++u) {
+        __syncthreads();  // (the staging, or the previous tile's epilogue, done with part)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    part[((wave * 4 + q) * ROWS + 16 * tt + 4 * (lane >> 4) + j) * 16 + (lane & 15)] = acc[4 * u + q][tt][j];
+        __syncthreads();
+        epilogue_moe<ROWS, 4, DR_MOE_GATE_UP_ROWS>(a, t0 + u, unit, ex, part, a.waves, 0.f);
+    }
+}
+
+__global__ __launch_bounds__(512) void dr_mfma_moe_pairs(const MoeArgs a) {
+    extern __shared__ float part[];  // the x staging during the K loop; then one tile's [W][4][32][16]
+    UnionLds* ul = union_lds<DR_MOE_GATE_UP_ROWS>();
+    moe_union(a, *ul);
+    const int tp2 = (a.tpe + 1) / 2;
+    const int unit = blockIdx.x / tp2, t0 = 2 * (blockIdx.x - unit * tp2);
+    const int ex = __builtin_amdgcn_readfirstlane(unit < ul->count ? (int)ul->list[unit] : -1);
+    if (ex < 0) return;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (a.tpe - t0 >= 2)
+        moe_pair_tiles<2>(a, t0, unit, ex, wave, lane, part);
+    else
+        moe_pair_tiles<1>(a, t0, unit, ex, wave, lane, part);
+}
+
 // ---- packing ---------------------------------------------------------------------------------------------------------
 
 // one face row (16 columns at one k) to block-float: the shared exponent is the largest biased fp32 exponent; each
@@ -2534,7 +2596,11 @@ hipError_t launch_moe(const MoeArgs& a, int mode, int rows, int pw, int grid, hi
                        : launch_gemv_moe<2, 4, DR_MOE_GATE_UP_ROWS>(a, grid, st);
             else if (rows == 16)
                 launch_mfma_moe<1, 4, DR_MOE_GATE_UP_ROWS>(a, grid, st);
-            else
+            else if (a.seg[0].fmt != DR_BFP4_KB && a.splits == 1) {
+                const size_t lds = max((size_t)a.waves * XS_BYTES, (size_t)a.waves * 4 * 32 * 16 * sizeof(float));
+                hipLaunchKernelGGL(dr_mfma_moe_pairs, dim3(a.tiles / a.tpe * ((a.tpe + 1) / 2)), dim3(64 * a.waves), lds,
+                                   st, a);
+            } else
                 launch_mfma_moe<2, 4, DR_MOE_GATE_UP_ROWS>(a, grid, st);
             break;
         default:

@@ -1,6 +1,6 @@
 """Benchmark of the dense_reader decode matmul on one MI355X.
 
-  python bench.py [--steps K] [--warmup W] [--config ns|c1|c2|c3|c4|c5|int4|moe|lm] [--no-cpu] [--cpu-seconds S]
+  python bench.py [--steps K] [--warmup W] [--config ns|c1|c2|c3|c4|c5|int4|moe|moe_rows|lm] [--no-cpu] [--cpu-seconds S]
   python bench.py --copy-probe      (a plain 256 MiB copy kernel: the byte counters' calibration under rocprofv3)
   python bench.py --read-probe BYTES  (the read ceiling: dr_stream_read of BYTES, timed as a config is)
   --no-eager: skip the eager timing loop (rocprofv3 traces then hold the graph-replayed launches but the warm-up's)
@@ -81,6 +81,15 @@ CONFIGS = {
         2880,
         [(2880, "bfp4", False)],
         {"moe": (32, 4, 2880, 2880)},
+    ),
+    "moe_rows": (
+        "MoE layer at 32 rows (verify / prefill), gpt-oss-20b shape: E=32, top-4 per row of random distinct experts, "
+        "H=I=2880, swiglu_oai with gate/up bias, bfp4 experts; a step is gate_up over the rows' union of experts "
+        "(moe8.gate_up_rows), then down (moe8.down_rows)",
+        32,
+        2880,
+        [(2880, "bfp4", False)],
+        {"moe": (32, 4, 2880, 2880), "rows": 32},
     ),
     "lm": (
         "LM head to token ids, M=4 K=4096 vocab=128256 bfp8: bf16 top-8 records, the best 16 rescored from the bf16 "
@@ -282,12 +291,27 @@ class Workload:
             self.set_wts.append(tw)
         self.x = (torch.randn(1, 1, 1, H, generator=g, device="cuda")).to(torch.bfloat16)
         tile = 576  # the reference's bytes of a BFP4_b tile
-        self.kbytes = k * (H // 32) * (2 * I // 32) * tile  # gate_up
-        self.wbytes = self.kbytes + k * (I // 32) * (H // 32) * tile  # + down
+        units = k
         self.copies = nsets
+        R = self.o.get("rows")
+        if R:  # R rows of random distinct experts each: the launches read the rows' union of experts once
+            gc = torch.Generator().manual_seed(1)
+            rid = torch.stack([torch.randperm(E, generator=gc)[:k] for _ in range(R)])
+            self.rows_ids = rid.to(torch.int16).reshape(1, 1, R, k).to("cuda")
+            self.rows_wts = torch.softmax(torch.randn(R, k, generator=gc), -1).to(torch.bfloat16).reshape(1, 1, R, k).to("cuda")
+            self.x = torch.randn(1, 1, R, H, generator=g, device="cuda").to(torch.bfloat16)
+            units = len(set(rid.flatten().tolist()))
+            self.copies = 1  # (the union's weights, units x 14 MB, are already past the 256 MB Infinity Cache)
+        self.kbytes = units * (H // 32) * (2 * I // 32) * tile  # gate_up
+        self.wbytes = self.kbytes + units * (I // 32) * (H // 32) * tile  # + down
         self.scales, self.res, self.rec, self.n = [None], None, None, H
 
     def kernel(self, i):
+        if self.o.get("rows"):
+            _, k, _, _ = self.moe_shape
+            self.moe8.gate_up_rows(self.x, self.P, self.rows_ids, self.rows_wts, k, self.o["rows"], act="swiglu_oai",
+                                   loaders=2)
+            return
         if self.o.get("moe"):
             _, k, _, _ = self.moe_shape
             s_ = i % self.copies
@@ -319,6 +343,11 @@ class Workload:
             L.matmul(self.x, ws[0], None, out=self.y)
 
     def step(self, i):
+        if self.o.get("rows"):
+            m8, (_, k, _, _), R = self.moe8, self.moe_shape, self.o["rows"]
+            h = m8.gate_up_rows(self.x, self.P, self.rows_ids, self.rows_wts, k, R, act="swiglu_oai", loaders=2)
+            m8.down_rows(h, self.P, self.rows_ids, k, R, loaders=2)
+            return
         if self.o.get("moe"):
             m8, (_, k, _, _) = self.moe8, self.moe_shape
             h = m8.route_gate_up(self.logits[i % self.copies], self.x, self.P, self.ids, self.wts, k,
@@ -450,7 +479,9 @@ def main():
             "weight_copies_rotated": wl.copies,
             **({"experts": wl.moe_shape[0], "top_k": wl.moe_shape[1], "hidden": wl.moe_shape[2],
                 "intermediate": wl.moe_shape[3], "pack": "kblock" if wl.kblock else "bfloat4_b",
-                "kernel": "route_gate_up (the routing and gate_up in one launch, the step's larger)"}
+                **({"rows": wl.o["rows"], "union_experts": wl.kbytes // (wl.moe_shape[2] // 32 * (2 * wl.moe_shape[3] // 32) * 576),
+                    "kernel": "gate_up_rows (the step's larger launch)"} if wl.o.get("rows") else
+                   {"kernel": "route_gate_up (the routing and gate_up in one launch, the step's larger)"})}
                if wl.o.get("moe") else {}),
             "timing": "HIP graph of the timed steps, replayed; events on the replay stream",
         },
@@ -485,17 +516,22 @@ def cpu_baseline(wl, seconds):
     if o.get("moe"):  # the reference's host check of the layer (moe8.py:642-660), float32, the k experts of a step
         gu, dn, bias = wl.host_w
         E, k, H, I = wl.moe_shape
-        xm = wl.x.reshape(1, H).cpu().float()
+        xm = wl.x.reshape(-1, H).cpu().float()
         wr = torch.full((k,), 1.0 / k)
 
-        def moe_step():
-            pre = torch.stack([xm[0] @ gu[e] for e in range(k)]) + bias.to(torch.bfloat16).float()
+        def moe_token(xr):
+            pre = torch.stack([xr @ gu[e] for e in range(k)]) + bias.to(torch.bfloat16).float()
             gc = pre[:, I:].clamp(max=7.0)
             h = gc * torch.sigmoid(1.702 * gc) * (pre[:, :I].clamp(-7.0, 7.0) + 1.0) * wr[:, None]
             return sum(h[e] @ dn[e] for e in range(k))
 
-        return _time_cpu(wl, moe_step, seconds, threads, "a float32 port of the reference's layer check (the k "
-                         "experts' gate_up, the clamped SwiGLU, the routing weights and down)")
+        R = o.get("rows")
+        if R:  # (every row through k experts, the first k of the pack's: the same work a row as the rows' own k)
+            return _time_cpu(wl, lambda: [moe_token(xm[r]) for r in range(R)], seconds, threads,
+                             f"a float32 port of the reference's layer check, {R} rows each through k experts "
+                             "(gate_up, the clamped SwiGLU, the routing weights and down)")
+        return _time_cpu(wl, lambda: moe_token(xm[0]), seconds, threads, "a float32 port of the reference's layer "
+                         "check (the k experts' gate_up, the clamped SwiGLU, the routing weights and down)")
     if o.get("int4"):  # the reference's host check: x (bf16) @ (q * s).T in float32 (int4/w4a16.py:100-107)
         hw = [O.int4_dequantized(w.codes.cpu(), w.scales.cpu()).float().T.contiguous() for w in wl.sets[0]]
     else:

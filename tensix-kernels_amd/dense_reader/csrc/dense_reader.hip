@@ -2644,8 +2644,8 @@ hipError_t launch_rows(const Args& a, int rows, int pw, int grid, hipStream_t st
         case 2: pw == 1 ? launch_gemv<2, 1>(a, grid, st) : pw == 2 ? launch_gemv<2, 2>(a, grid, st) : launch_gemv<2, 4>(a, grid, st); break;
         case 4: pw == 2 ? launch_gemv<4, 2>(a, grid, st) : launch_gemv<4, 4>(a, grid, st); break;
         case 8: launch_gemv<8, 2>(a, grid, st); break;  // (a GLU pass takes at most 4 GEMV rows)
-        case 16: pw == 2 ? launch_mfma<1, 2>(a, grid, st) : launch_mfma<1, 4>(a, grid, st); break;
-        default: launch_mfma<2, 2>(a, grid, st); break;  // (a GLU pass takes at most 16 MFMA rows)
+        case 16: pw == 1 ? launch_mfma<1, 1>(a, grid, st) : pw == 2 ? launch_mfma<1, 2>(a, grid, st) : launch_mfma<1, 4>(a, grid, st); break;
+        default: pw == 1 ? launch_mfma<2, 1>(a, grid, st) : launch_mfma<2, 2>(a, grid, st); break;  // (a GLU pass takes at most 16 MFMA rows)
     }
     return hipGetLastError();
 }
@@ -2846,7 +2846,11 @@ int prepare(const dr_launch* L, Args& a, int& pw, int& tiles, int& mr, bool gath
     // 32-column tiles than CUs, or a count just past a multiple of the CUs): each column's sums are made by the same
     // lanes in the same order whatever the tile width, so the results are the same bit for bit. (Not with top-k
     // records, one a 32-column tile, nor a GLU's pairs.)
-    if (!gather && pw == 2 && mr <= 2 && a.rec == nullptr && narrow_better(tiles)) {
+    // The MFMA kernel (unsplit) takes them where even the 16-column tiles are at most one a CU: each reads all of x, so
+    // two on a CU cost more than one 32-column tile (bfloat8_b K = 4096 at 3-16 rows, N = 2048 and 4096: 16-19 %
+    // faster; the same sums a column, as the GEMV's).
+    if (!gather && pw == 2 && a.rec == nullptr &&
+        (mr <= 2 ? narrow_better(tiles) : (mr >= 16 && a.splits == 1 && 2 * tiles <= cu_count()))) {
         pw = 1;
         tiles = 0;
         for (int i = 0; i < a.nseg; ++i) {
@@ -2855,7 +2859,7 @@ int prepare(const dr_launch* L, Args& a, int& pw, int& tiles, int& mr, bool gath
             tiles += a.seg[i].tiles;
         }
         a.tiles = tiles;
-        plan(L->k, false, &a.chunks, &a.kch, &a.waves, &a.splits, &a.cps);
+        plan(L->k, mr >= 16, &a.chunks, &a.kch, &a.waves, &a.splits, &a.cps);
         limit_splits(a);
     }
     // 32 rows, plain tiles, more tiles than CUs: block-float segments in tile pairs (dr_mfma_pairs)

@@ -299,6 +299,26 @@ def test_rows32_staged_x(device, fmt):
 
 
 @pytest.mark.parametrize("fmt", ["bfp8", "bfp4", "bf16"])
+def test_mfma_narrow_tiles_bitwise(device, fmt):
+    """An unsplit MFMA launch of few tiles runs 16-column tiles (`launch_plan` says which): a weight of 96 tiles alone
+    (16-column) against the same weight in a block list of 256 tiles (32-column), bit for bit, at 8 and 32 rows."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    k = 2048
+    wa, wb = matrix(96 * 32, k, 150), matrix(max(160, cus - 96 + 1) * 32, k, 151)
+    ta, _ = linear.native_weight(device, wa, DTYPES[fmt])
+    tb, _ = linear.native_weight(device, wb, DTYPES[fmt])
+    na, nb = wa.shape[0], wb.shape[0]
+    for m in (8, 32):
+        x, tx = x_input(device, m, k, 152 + m)
+        assert linear.launch_plan(tx, ta, None)["tile_cols"] == (16 if 2 * 96 <= cus else 32)
+        assert linear.launch_plan(tx, [(ta, 0), (tb, 96)], None)["tile_cols"] == 32
+        one = host(linear.matmul(tx, ta, None), m, na)
+        check(f"{fmt} rows {m}: 96 tiles alone", one, ref(x, held(ta, na)))
+        both = host(linear.matmul(tx, [(ta, 0), (tb, 96)], None), m, na + nb)
+        same(f"{fmt} rows {m}: 16-column tiles against the 32-column block list", both[:, :na], one)
+
+
+@pytest.mark.parametrize("fmt", ["bfp8", "bfp4", "bf16"])
 def test_rows_in_passes_bitwise(device, fmt):
     """Past 32 rows the launch runs passes of 32 (a last pass of at most 16 rows on the 16-row kernel): each pass's rows
     equal bit for bit those of a call on those rows alone, and the 16- and 32-row kernels sum a row alike. At 300 tiles

@@ -284,23 +284,27 @@ __device__ __forceinline__ void chunk_bfp8(const Args& a, const uint8_t* const* 
     }
 }
 
-// The nibble u = m + 8 enters a dot2c as the bf16 whose high byte is HI and low byte u: HI = 0x43 gives 128 + u = 136 + m
-// (x as it is: int4), HI = 0x3F gives (128 + u) / 256 (the folded x' of bfloat4_b, which can be as large as the
-// format allows: its products and their excess over x' m stay 2^8 further from fp32's overflow).
+// The nibble u = m + 8 enters a dot2c as the bf16 whose high byte is HI and low byte u (u < 16, so the exponent field
+// is 2 (HI & 0x7F) and u the mantissa): HI = 0x43 gives 128 + u = 136 + m (x as it is: int4), HI = 0x3F gives
+// (128 + u) / 256 (the folded x' of bfloat4_b, which can be as large as the format allows: its products and their
+// excess over x' m stay 2^8 further from fp32's overflow), HI = 0x1F gives (128 + u) 2^-72 (the fold of a panel chunk
+// of small shared exponents, whose x' carries the 2^64 taken off here).
 constexpr uint32_t BF16_136 = 0x43434343u;
 constexpr uint32_t BF16_136_256 = 0x3F3F3F3Fu;
+constexpr uint32_t BF16_136_2P72 = 0x1F1F1F1Fu;
 
-template <int D, int MR, int PW, uint32_t MAGIC = BF16_136>
-__device__ __forceinline__ void bfp4_step(float (&acc)[PW][MR], const uint32_t (&xs)[PW][MR], const uint4 (&c)[PW]) {
+template <int D, int MR, int PW>
+__device__ __forceinline__ void bfp4_step(float (&acc)[PW][MR], const uint32_t (&xs)[PW][MR], const uint4 (&c)[PW],
+                                          const uint32_t (&mg)[PW]) {
 #pragma unroll
     for (int q = 0; q < PW; ++q) {
         const uint32_t w = D == 0 ? c[q].x : D == 1 ? c[q].y : D == 2 ? c[q].z : c[q].w;
         const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
-        // bf16 pairs MAGIC-byte:u, for k 8D + (0,1), (2,3) (low nibbles) and (4,5), (6,7) (high)
-        const uint32_t a0 = __builtin_amdgcn_perm(MAGIC, lo, 0x04010400u);
-        const uint32_t a1 = __builtin_amdgcn_perm(MAGIC, lo, 0x04030402u);
-        const uint32_t a2 = __builtin_amdgcn_perm(MAGIC, hi, 0x04010400u);
-        const uint32_t a3 = __builtin_amdgcn_perm(MAGIC, hi, 0x04030402u);
+        // bf16 pairs of panel q's magic byte above u, for k 8D + (0,1), (2,3) (low nibbles) and (4,5), (6,7) (high)
+        const uint32_t a0 = __builtin_amdgcn_perm(mg[q], lo, 0x04010400u);
+        const uint32_t a1 = __builtin_amdgcn_perm(mg[q], lo, 0x04030402u);
+        const uint32_t a2 = __builtin_amdgcn_perm(mg[q], hi, 0x04010400u);
+        const uint32_t a3 = __builtin_amdgcn_perm(mg[q], hi, 0x04030402u);
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
             dot2_bcast<4 * D + 0, D == 0>(acc[q][m], xs[q][m], a0);
@@ -313,7 +317,7 @@ __device__ __forceinline__ void bfp4_step(float (&acc)[PW][MR], const uint32_t (
                 dot2_bcast<4 * D + 3, false>(acc[q][m], xs[q][m], a3);
         }
     }
-    if constexpr (D + 1 < 4) bfp4_step<D + 1, MR, PW, MAGIC>(acc, xs, c);
+    if constexpr (D + 1 < 4) bfp4_step<D + 1, MR, PW>(acc, xs, c, mg);
 }
 
 // the 128-K block whose codes a bfloat4_b decoder loads for block b: b itself, or where b lies wholly in the padding
@@ -326,6 +330,14 @@ __device__ __forceinline__ int real_block(int b, int k) { return b * 128 >= k ? 
 // m) / 256 and sx (per lane, the x' it made) gives the (136 / 256) sum x' to take off; the caller scales the chunk's
 // difference by 256 (exact: the same value, rounded alike, as with the weights 136 + m, until those would overflow).
 // One chunk of one or two exponent groups (two blocks each), loaded as chunk_bfp8 loads its chunk.
+//
+// x' = x 2^(E - 129) is a bf16 denormal, and loses low bits of x, below E + log2|x| = 3. So a panel whose shared
+// exponents in the wavefront's chunk are all below 64 folds x' = x 2^(E - 65) instead, a normal bf16 for any |x| above
+// 2^-62, against the weights (136 + m) 2^-72: every product is the same value, and sx, the x' sum, is scaled back by
+// 2^-64 at the end. For a chunk of normal values the two folds give the same bits (powers of two scale exactly); the
+// choice is one ballot a panel, uniform across the wavefront, so every lane of a row sums one kind of x'. A panel chunk
+// with an exponent of 64 or more keeps the plain fold: its products then lie at least 2^60 above any that a denormal x'
+// could hold.
 template <int MR, int PW, bool ONEG = false>
 __device__ __forceinline__ void chunk_bfp4(const Args& a, const uint8_t* const* cb, const uint8_t* const* eb, int k0,
                                            int k1, int lane, float (&acc)[PW][MR], float (&sx)[PW][MR]) {
@@ -360,6 +372,17 @@ __device__ __forceinline__ void chunk_bfp4(const Args& a, const uint8_t* const* 
 #pragma unroll
         for (int q = 0; q < PW; ++q) c[u].c[q] = ld_stream16(cb[q] + (uint32_t)(b * 1024 + lane * 16));
     }
+    // the fold of each panel: every shared exponent of the chunk below 64 (no byte with either of its top two bits set)
+    uint32_t mg[PW];
+    int eb0[PW];
+    bool small[PW];
+#pragma unroll
+    for (int q = 0; q < PW; ++q) {
+        const uint32_t any = e[0][q] | e[NU / 2 - 1][q];
+        small[q] = __builtin_amdgcn_ballot_w64((any & 0xC0C0C0C0u) != 0u) == 0ull;
+        mg[q] = small[q] ? BF16_136_2P72 : BF16_136_256;
+        eb0[q] = small[q] ? 65 : 129;
+    }
 #pragma unroll
     for (int u = 0; u < NU; ++u) {
         if (u == 2 && !two) break;
@@ -369,8 +392,8 @@ __device__ __forceinline__ void chunk_bfp4(const Args& a, const uint8_t* const* 
             const uint32_t ep = e[u >> 1][q] >> (16 * (u & 1));
 #pragma unroll
             for (int m = 0; m < MR; ++m) {
-                const float f0 = __builtin_ldexpf(bf16_to_f32(xp[u][m] & 0xFFFFu), (int)(ep & 0xFFu) - 129);
-                const float f1 = __builtin_ldexpf(bf16_to_f32(xp[u][m] >> 16), (int)((ep >> 8) & 0xFFu) - 129);
+                const float f0 = __builtin_ldexpf(bf16_to_f32(xp[u][m] & 0xFFFFu), (int)(ep & 0xFFu) - eb0[q]);
+                const float f1 = __builtin_ldexpf(bf16_to_f32(xp[u][m] >> 16), (int)((ep >> 8) & 0xFFu) - eb0[q]);
                 // exact: x has 8 significant bits and a power of two keeps them (a denormal result may lose some;
                 // sx then adds the same truncated values the dot products see)
                 const uint32_t p = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xFFFF0000u);
@@ -378,9 +401,13 @@ __device__ __forceinline__ void chunk_bfp4(const Args& a, const uint8_t* const* 
                 sx[q][m] += bf16_to_f32(p & 0xFFFFu) + bf16_to_f32(p >> 16);
             }
         }
-        bfp4_step<0, MR, PW, BF16_136_256>(acc, xs, c[u].c);
+        bfp4_step<0, MR, PW>(acc, xs, c[u].c, mg);
     }
     dot_fence(acc);
+#pragma unroll
+    for (int q = 0; q < PW; ++q)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) sx[q][m] = __builtin_ldexpf(sx[q][m], small[q] ? -64 : 0);
 }
 
 // a bfloat4_b chunk's column sum (the wavefront's lanes reduced) less the excess: (acc - (136 / 256) sum x') * 256
@@ -549,7 +576,10 @@ __device__ __forceinline__ void chunk_int4(const Args& a, const uint8_t* const* 
         for (int q = 0; q < PW; ++q)
 #pragma unroll
             for (int m = 0; m < MR; ++m) t[q][m] = 0.f;
-        bfp4_step<0, MR, PW>(t, xs, c[u].c);
+        uint32_t mg[PW];
+#pragma unroll
+        for (int q = 0; q < PW; ++q) mg[q] = BF16_136;
+        bfp4_step<0, MR, PW>(t, xs, c[u].c, mg);
         dot_fence(t);
 #pragma unroll
         for (int q = 0; q < PW; ++q)

@@ -114,6 +114,33 @@ def test_ns_graph_replay(device, ns_weights):
         torch.cuda.synchronize()
 
 
+# --- C1: bfloat8_b M=1 K=2048 N=4096, no fused stage ---------------------------------------------------------------
+
+
+def test_c1_gemv(device):
+    """C1 as the bench times it: x [1, 2048] against bfloat8_b W [4096, 2048], no scale, bf16 out, on dr_gemv_g1 (256-k
+    chunks) with 16-column tiles (256 workgroups), against the oracle; repeated calls bit-identical, and the same bits
+    as a launch of 32-column tiles (the weight as the first block of a list wide enough for them)."""
+    k, n, m = 2048, 4096, 1
+    wt = O.matrix(n, k, 130)
+    tw = linear.native_weight(device, wt, linear.bfloat8_b)[0]
+    held = pinned_held(tw, wt, "bfp8", n)
+    x, tx = x_input(device, m, k, 131)
+    p = linear.launch_plan(tx, tw, None)
+    assert_plan(p, kernel="gemv", rows_per_pass=1, tile_cols=16, tiles=256, kch=256, splits=1)
+    y = linear.matmul(tx, tw, None)
+    check(f"C1 bfp8 rows {m} K {k} N {n}", host(y, m, n), ref64(x, held).float())
+    same("C1: repeated call", host(linear.matmul(tx, tw, None), m, n), host(y, m, n))
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    wide_tiles = 7 * cus // 4  # (448 on 256 CUs: a launch of 32-column tiles)
+    big = linear.native_weight(device, O.matrix(32 * wide_tiles - n, k, 132), linear.bfloat8_b)[0]
+    blocks = [(tw, 0), (big, n // 32)]
+    pb = linear.launch_plan(tx, blocks, None)
+    assert_plan(pb, kernel="gemv", tile_cols=32, kch=256, tiles=wide_tiles)
+    yb = host(linear.matmul(tx, blocks, None), m, n)
+    same("C1: 16-column tiles against 32-column tiles (the weight inside a wider block list)", yb, host(y, m, n))
+
+
 @pytest.mark.parametrize("m", [1, 2])
 def test_int4_wide(device, m):
     """int4 W4A16 at the bench's K=4096 N=14336 (the wide GEMV), against the oracle's x @ (q * s).T."""
@@ -255,12 +282,11 @@ def ids_match_with_ties(name, got_scores, want_scores, rel=1e-3):
     assert not bad.any(), name
 
 
-def test_c5_topk_records(device):
-    """x [4, 4096] against bfloat8_b W [128256, 4096]: fp32 top-8 records of every row, then the global top-32 (the
-    bench's c5). Record ids against the float64 logits (exact except ties within 1e-3 rel), record scores against the
-    float64 logits (rel 1e-3), record values rounded to bf16 equal y at their ids, the merge against the oracle's merge
-    of the records and its ids against the float64 global top-32."""
-    k, n, m, kk = 4096, 128256, 4, 8
+@pytest.fixture(scope="module")
+def c5_case(device):
+    """C5's weight (bfloat8_b [128256, 4096], its held tiles pinned against the oracle), x [4, 4096], and the float64
+    logits x @ held [4, 128256]."""
+    k, n, m = 4096, 128256, 4
     wt = O.matrix(n, k, 190)
     tw = linear.native_weight(device, wt, linear.bfloat8_b)[0]
     h = pinned_held(tw, wt, "bfp8", n)
@@ -269,17 +295,41 @@ def test_c5_topk_records(device):
     xb = x.to(torch.bfloat16).double()
     s64 = torch.cat([xb @ h[:, c : c + 16384].double() for c in range(0, n, 16384)], dim=1).numpy()  # [m, n]
     del h
-    slots = linear.topk_slots(n)
-    r = linear.topk_result(device, slots, m, kk)
-    spec = {"r": r, "k": kk, "rows": m, "slot0": 0, "base": 0, "n": n, "write_y": True, "fp32": True}
+    return k, n, m, tw, tx, s64
+
+
+@pytest.mark.parametrize("layout", ["per_tile", "grouped"])
+def test_c5_topk_records(device, c5_case, layout):
+    """x [4, 4096] against bfloat8_b W [128256, 4096]: fp32 top-8 records of every row, then the global top-32.
+    "per_tile" is the bench's c5 call exactly ("slots": 0, write_y off): one record a 32-column tile, 4008 records, and
+    the merge over all 4008; "grouped" the default slots (grid_slots()), tiles ranked together in groups. Record ids
+    against the float64 logits of their columns (exact except ties within 1e-3 rel), record scores against the float64
+    logits (rel 1e-3), the records bit for bit those of the same call with write_y on, record values rounded to bf16
+    equal y at their ids, the merge against the oracle's merge of the records and its ids against the float64 global
+    top-32."""
+    k, n, m, tw, tx, s64 = c5_case
+    kk = 8
+    tiles = -(-n // 32)
+    slots = 0 if layout == "per_tile" else None
+    nrec = linear.topk_slots(n, slots)
+    r = linear.topk_result(device, nrec, m, kk)
+    spec = {"r": r, "k": kk, "rows": m, "slot0": 0, "base": 0, "n": n, "write_y": False, "fp32": True}
+    if slots is not None:
+        spec["slots"] = slots
     p = linear.launch_plan(tx, tw, None, topk=spec)
     assert_plan(p, kernel="mfma", rows_per_pass=16)
     per = p["tiles_per_record"]
-    nrec = p["records"]
-    assert per >= 1 and nrec == -(-(n // 32) // per) and nrec <= slots, p
-    y = host(linear.matmul(tx, tw, None, topk=spec), m, n)
+    if layout == "per_tile":
+        assert nrec == tiles == 4008 and p["records"] == 4008 and per == 1, p
+    else:
+        assert per > 1 and p["records"] == nrec == -(-tiles // per) and nrec <= linear.grid_slots(), p
+    linear.matmul(tx, tw, None, topk=spec)
+    rw = r.clone()
+    r.zero_()
+    y = host(linear.matmul(tx, tw, None, topk={**spec, "write_y": True}), m, n)
+    same(f"C5 {layout}: records with write_y off equal those with it on", rw.cpu(), r.cpu())
     check(f"C5 y rows {m} N {n}", y, torch.from_numpy(s64).float())
-    vals, ids = linear.topk_records(r[:, :, :nrec], m, kk, fp32=True)
+    vals, ids = linear.topk_records(rw, m, kk, fp32=True)
     vals, ids = vals.numpy().reshape(m, nrec, kk), ids.numpy().reshape(m, nrec, kk)
     assert (ids >= 0).all(), "C5: every record slot is filled (each record spans at least 32 columns)"
     span = 32 * per
@@ -290,16 +340,17 @@ def test_c5_topk_records(device):
     pad = nrec * span - n
     sp = np.concatenate([s64, np.full((m, pad), -np.inf)], axis=1).reshape(m, nrec, span)
     want = _sorted_desc(sp, 2)[:, :, :kk]
-    ids_match_with_ties("C5 record ids against the float64 logits", _sorted_desc(got, 2), want)
-    check("C5 record scores against the float64 logits", torch.from_numpy(vals.reshape(-1)),
+    ids_match_with_ties(f"C5 {layout}: record ids against the float64 logits", _sorted_desc(got, 2), want)
+    check(f"C5 {layout}: record scores against the float64 logits", torch.from_numpy(vals.reshape(-1)),
           torch.from_numpy(got.reshape(-1)).float(), rel=1e-3, pcc=0.999999)
     yb = y.numpy()
     at = np.take_along_axis(yb, ids.reshape(m, -1), axis=1).reshape(m, nrec, kk)
-    same("C5 record values rounded to bf16 equal y at their ids",
+    same(f"C5 {layout}: record values rounded to bf16 equal y at their ids",
          torch.from_numpy(vals).to(torch.bfloat16).float(), torch.from_numpy(at))
-    gv, gi = linear.topk_merge(r, m, kk, k_out=32, fp32=True, records=nrec)
+    gv, gi = linear.topk_merge(rw, m, kk, k_out=32, fp32=True)
     wv, wi = O.global_topk(vals.reshape(m, -1), ids.reshape(m, -1), 32)
-    same("C5 global top-32 values against the oracle's merge of the records", gv.cpu(), torch.from_numpy(wv))
-    same("C5 global top-32 ids against the oracle's merge of the records", gi.cpu().long(), torch.from_numpy(wi))
+    same(f"C5 {layout}: global top-32 values against the oracle's merge of the records", gv.cpu(), torch.from_numpy(wv))
+    same(f"C5 {layout}: global top-32 ids against the oracle's merge of the records", gi.cpu().long(),
+         torch.from_numpy(wi))
     g64 = np.take_along_axis(s64, gi.cpu().numpy().astype(np.int64), axis=1)
-    ids_match_with_ties("C5 global top-32 ids against the float64 logits", g64, _sorted_desc(s64, 1)[:, :32])
+    ids_match_with_ties(f"C5 {layout}: global top-32 ids against the float64 logits", g64, _sorted_desc(s64, 1)[:, :32])

@@ -4,7 +4,7 @@ The config tests pin each benchmarked shape; this sweep covers the combinations 
 kernel (1-2 GEMV, 3-32 MFMA, past 32 in passes), K with and without padding and split K, N off the tile width, bf16
 and fp32 column scales, the GLU (interleaved or two weights, silu or gelu_tanh, with or without scales), the residual
 in both modes with and without the fp32 output, the fp32 output alone, col0 into a wider output, block lists of mixed
-formats with per-block scales, and top-k records (bf16 keys, a record a tile or groups of tiles). Expected values come
+formats with per-block scales, and top-k records (bf16 keys or fp32 scores, a record a tile or groups of tiles). Expected values come
 from the oracle alone (oracle.held of the float weights, oracle.ref in float64, oracle.tile_topk's ranking of the op's
 own output), with the reference's bars (linear.py / test_dense_reader.py: 1 % relative Frobenius error and PCC 0.9999
 for bf16 outputs, 0.1 % for fp32 outputs, records bit for bit); every case is also called twice and must repeat bit
@@ -62,6 +62,7 @@ def _case(i):
         c["cut"] = int(r.integers(0, 40)) if r.integers(2) else 0  # (valid columns: n - cut)
         c["base"] = int(r.integers(0, 5000))
         c["slots"] = int(r.choice([0, 3, 7]))  # (0: a record a tile; else tiles ranked in groups)
+        c["fp32"] = bool(r.integers(2))  # (fp32 scores, or the reference's bf16 keys)
     if c["k"] >= 9216:
         c["n"] = min(c["n"], 256)  # (a split-K case: the oracle's float64 product stays small)
     return c
@@ -172,18 +173,25 @@ def test_sweep(device, i):
         same(f"{name} col0 {c0}: the other columns untouched", rest, torch.full_like(rest, 7.0))
     elif kind == "topk":
         tw, h = _weight(device, n, k, fmt, 3000 + i)
-        rows, kk, base, slots = c["rows"], c["kk"], c["base"], c["slots"]
+        rows, kk, base, slots, f32 = c["rows"], c["kk"], c["base"], c["slots"], c["fp32"]
         nv = max(1, n - c["cut"])
         recs = linear.topk_slots(n, slots)
         r = linear.topk_result(device, recs, rows, kk)
-        spec = {"r": r, "k": kk, "rows": rows, "slot0": 0, "base": base, "n": nv, "write_y": True, "slots": slots}
+        spec = {"r": r, "k": kk, "rows": rows, "slot0": 0, "base": base, "n": nv, "write_y": True, "slots": slots,
+                "fp32": f32}
         g = linear.launch_plan(tx, tw, None, topk=spec)["tiles_per_record"]
         y = _host(linear.matmul(tx, tw, None, topk=spec), m, n)
         check(f"{name} top-k: y", y, _ref64(x, h).float())
         words = r.cpu().reshape(recs, -1)
-        want = O.tile_topk(y[:rows].numpy(), rows, kk, nv, base, width=32 * g)
-        same(f"{name} top-k rows {rows} k {kk} valid {nv} groups of {g}: records against the oracle's ranking of y",
-             words, torch.from_numpy(want.view(np.int32)))
+        yf = None
+        if f32:  # the fp32 scores the records rank: the same sums, written by an fp32-output call
+            yf = _host(linear.matmul(tx, tw, None, out32=True), m, n)
+            check(f"{name} top-k: fp32 scores", yf, _ref64(x, h).float(), rel=1e-3, pcc=0.999999)
+            same(f"{name} top-k: fp32 scores rounded to bf16 equal y", yf.to(torch.bfloat16).float(), y)
+            yf = yf[:rows].numpy()
+        want = O.tile_topk(y[:rows].numpy(), rows, kk, nv, base, fp32=f32, yf=yf, width=32 * g)
+        same(f"{name} top-k rows {rows} k {kk} valid {nv} groups of {g} fp32 {f32}: records against the oracle's "
+             f"ranking of y", words, torch.from_numpy(want.view(np.int32)))
         r2 = linear.topk_result(device, recs, rows, kk)
         linear.matmul(tx, tw, None, topk={**spec, "r": r2})
         same(f"{name} top-k: repeated call", r2.cpu().reshape(recs, -1), words)

@@ -122,7 +122,7 @@ typedef struct dr_topk {
 } dr_topk;
 
 typedef struct dr_launch {
-    const void* x;       /* [m][ldx] bf16 */
+    const void* x;       /* [m][ldx] bf16, 16-byte aligned, ldx a multiple of 8 (rows are read 16 bytes at a time) */
     int32_t m, k, ldx;
     void* y;             /* [m][ldy] bf16 or fp32 */
     int32_t ldy;

@@ -239,48 +239,115 @@ __device__ __forceinline__ void bfp8_step(float (&acc)[PW][MR], const float (&xs
     if constexpr (I + 1 < 16) bfp8_step<I + 1, MR, PW>(acc, xs, c);
 }
 
+// ---- x through LDS: a wavefront's rows over its chunk ---------------------------------------------------------------
+//
+// A wavefront stages the x its chunk needs (MR rows over 512 k) in an LDS window of its own with one 16-byte load a lane
+// a row, instead of one 2-byte load a lane per 64-k block: the block loaders then read x from LDS. (Fewer vector
+// memory instructions: in a copy of the north-star GEMV on MI355X the small x loads cost 0.3 us of 11.4.) x rows are
+// 16-byte aligned and K is a multiple of 32 (the host checks both), so a lane's 8 values lie wholly inside or wholly
+// past K.
+constexpr int XWIN = 512;  // k a window holds: the longest chunk
+template <int MR>
+struct XWin {
+    uint4 v[MR];
+};
+// lane l's 16 bytes of each row: k0 + 8 l .. + 7 (zeros past K or past x's rows)
+template <int MR>
+__device__ __forceinline__ XWin<MR> x_win_load(const Args& a, int k0, int lane) {
+    XWin<MR> w;
+    const int k = k0 + 8 * lane, kc = min(k, a.k - 8);
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        const int mc = min(m, a.m - 1);
+        const uint4 v = *reinterpret_cast<const uint4*>(a.x + (size_t)mc * a.ldx + kc);
+        const uint32_t keep = opaque((k < a.k && m < a.m) ? 0xFFFFFFFFu : 0u);
+        w.v[m] = make_uint4(v.x & keep, v.y & keep, v.z & keep, v.w & keep);
+    }
+    return w;
+}
+// (LDS instructions of one wavefront execute in order: its later reads see these writes)
+template <int MR>
+__device__ __forceinline__ void x_win_store(const XWin<MR>& w, uint16_t (*xl)[XWIN], int lane) {
+#pragma unroll
+    for (int m = 0; m < MR; ++m) *reinterpret_cast<uint4*>(&xl[m][8 * lane]) = w.v[m];
+}
+
+// ---- the block loaders: rotated slots, a few in flight ---------------------------------------------------------------
+//
+// A chunk's blocks are loaded and summed in slots: slot u of panel q holds the chunk's block (u + rot_q) mod nb, with
+// rot_q = c + (nb_max / 2) (p_q & 1), c = k0 / the chunk length (the chunk's index) and p_q the panel's index in its
+// weight. Rotating by the chunk
+// spreads the addresses that the wavefronts of the launch request at one time (the first slot of every wavefront is
+// not the first block of every chunk), and the half-turn for odd panels spreads a tile's two panels; on MI355X the
+// north-star read went 10.3 -> 10.0 us with that order alone. The slots are summed in slot order, a function of the
+// chunk and the panel's parity only, so every launch of a weight sums each column in the same order (block lists,
+// 16- and 32-column tiles, split K). The first D slots' codes are issued with x and the exponents; slot u + D's are
+// issued before slot u is decoded (scheduling barriers keep that order), so a wavefront keeps D slots in flight
+// and its data arrives spread over the launch: with all eight issued at once they landed in one burst, and the last
+// wavefronts' whole decode came after the last byte (0.3 us of 11.4 in the copy).
+// Slots in flight a wavefront: about 6 KB of bfloat8_b codes or 4 KB of bfloat4_b / int4 codes (a slot is one KB a
+// panel). Measured on MI355X (alternating builds in one process): the north star (2 panels) 11.71 / 11.66 / 11.86 us
+// with 2 / 3 / 4 slots; the bfloat4_b GLU pair (4 panels) 13.79 / 14.02 / 14.20 / 14.31 us with 1 / 2 / 3 / 4.
+template <int PW>
+__host__ __device__ constexpr int depth_bfp8() {
+    return PW >= 6 ? 1 : 6 / PW;
+}
+template <int PW>
+__host__ __device__ constexpr int depth_bfp4() {
+    return PW >= 4 ? 1 : 4 / PW;
+}
+
 // bfp8: lane (kq, c) accumulates column c over k = 64 b + 16 kq + i; lane (kq, i) makes x' for that k. One chunk
-// [k0, k1) of one or two exponent groups (256 k each): x first, then the exponents, then the codes are issued (waits
-// are in issue order, so x' is made before the codes arrive). ONEG: every chunk of the launch is one group (256-k
-// chunks), and only that group is loaded; otherwise a one-group chunk (the last of a K that is an odd number of
-// groups) loads its group twice (the second copy is never used) so that no load sits under a branch.
+// [k0, k1) of one or two exponent groups (256 k each). ONEG: every chunk of the launch is one group (256-k chunks), and
+// only that group is loaded; otherwise a one-group chunk (the last of a K that is an odd number of groups) loads its
+// group twice (the second copy is never used) so that no load sits under a branch.
 template <int MR, int PW, bool ONEG = false>
-__device__ __forceinline__ void chunk_bfp8(const Args& a, const uint8_t* const* cb, const uint8_t* const* eb, int k0,
-                                           int k1, int lane, float (&acc)[PW][MR]) {
-    constexpr int NU = ONEG ? 4 : 8;  // 64-k blocks loaded
+__device__ __forceinline__ void chunk_bfp8(const Args& a, const uint8_t* const* cb, const uint8_t* const* eb,
+                                           const int (&par)[PW], int k0, int k1, int lane,
+                                           uint16_t (*xl)[XWIN], float (&acc)[PW][MR]) {
+    constexpr int NU = ONEG ? 4 : 8;  // 64-k blocks (slots)
+    constexpr int D = depth_bfp8<PW>() < NU ? depth_bfp8<PW>() : NU;
     const int g0 = k0 >> 8;
     const bool two = !ONEG && k1 - k0 > 256;
-    const int g1 = two ? g0 + 1 : g0;
-    uint32_t xb[NU][MR];
-    uint32_t e[NU / 4][PW];
+    const int nb = two ? NU : 4;
+    int rot[PW];
+#pragma unroll
+    for (int q = 0; q < PW; ++q) rot[q] = ((k0 >> (ONEG ? 8 : 9)) + (NU / 2) * par[q]) & (nb - 1);
+    const XWin<MR> xw = x_win_load<MR>(a, k0, lane);
+    uint64_t e[PW];  // the chunk's exponents of panel q: byte j (of 8, or 4) is block j's, for the lane's k
+#pragma unroll
+    for (int q = 0; q < PW; ++q) {
+        const uint32_t lo = ld_stream4(eb[q] + (uint32_t)(g0 * 256 + 4 * lane));
+        const uint32_t hi = ld_stream4(eb[q] + (uint32_t)((two ? g0 + 1 : g0) * 256 + 4 * lane));
+        e[q] = (uint64_t)lo | ((uint64_t)hi << 32);
+    }
     Codes<PW> c[NU];
+    auto issue = [&](int u) {
+#pragma unroll
+        for (int q = 0; q < PW; ++q) {
+            const int b = 4 * g0 + ((u + rot[q]) & (nb - 1));
+            c[u].c[q] = ld_stream16(cb[q] + (uint32_t)(b * 1024 + lane * 16));
+        }
+    };
+#pragma unroll
+    for (int u = 0; u < D; ++u) issue(u);
+    x_win_store<MR>(xw, xl, lane);
 #pragma unroll
     for (int u = 0; u < NU; ++u) {
-        const int b = 4 * (u < 4 ? g0 : g1) + (u & 3);
+        if (u + D < NU) issue(u + D);
+        __builtin_amdgcn_sched_barrier(0);
+        if (ONEG || u < nb) {
+            float xs[PW][MR];
 #pragma unroll
-        for (int m = 0; m < MR; ++m) xb[u][m] = x_bits(a, m, b * 64 + lane);
-    }
+            for (int q = 0; q < PW; ++q) {
+                const int b = (u + rot[q]) & (nb - 1);
+                const int ev = (int)((uint32_t)(e[q] >> (8 * b)) & 0xFFu) - 133;
 #pragma unroll
-    for (int h = 0; h < NU / 4; ++h)
-#pragma unroll
-        for (int q = 0; q < PW; ++q)
-            e[h][q] = ld_stream4(eb[q] + (uint32_t)((h ? g1 : g0) * 256 + 4 * lane));
-#pragma unroll
-    for (int u = 0; u < NU; ++u) {
-        const int b = 4 * (u < 4 ? g0 : g1) + (u & 3);
-#pragma unroll
-        for (int q = 0; q < PW; ++q) c[u].c[q] = ld_stream16(cb[q] + (uint32_t)(b * 1024 + lane * 16));
-    }
-#pragma unroll
-    for (int u = 0; u < NU; ++u) {
-        if (u == 4 && !two) break;
-        float xs[PW][MR];
-#pragma unroll
-        for (int q = 0; q < PW; ++q)
-#pragma unroll
-            for (int m = 0; m < MR; ++m)
-                xs[q][m] = __builtin_ldexpf(bf16_to_f32(xb[u][m]), (int)((e[u >> 2][q] >> (8 * (u & 3))) & 0xFFu) - 133);
-        bfp8_step<0, MR, PW>(acc, xs, c[u].c);
+                for (int m = 0; m < MR; ++m) xs[q][m] = __builtin_ldexpf(bf16_to_f32(xl[m][64 * b + lane]), ev);
+            }
+            bfp8_step<0, MR, PW>(acc, xs, c[u].c);
+        }
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -339,69 +406,71 @@ __device__ __forceinline__ int real_block(int b, int k) { return b * 128 >= k ? 
 // with an exponent of 64 or more keeps the plain fold: its products then lie at least 2^60 above any that a denormal x'
 // could hold.
 template <int MR, int PW, bool ONEG = false>
-__device__ __forceinline__ void chunk_bfp4(const Args& a, const uint8_t* const* cb, const uint8_t* const* eb, int k0,
-                                           int k1, int lane, float (&acc)[PW][MR], float (&sx)[PW][MR]) {
-    constexpr int NU = ONEG ? 2 : 4;  // 128-k blocks loaded
+__device__ __forceinline__ void chunk_bfp4(const Args& a, const uint8_t* const* cb, const uint8_t* const* eb,
+                                           const int (&par)[PW], int k0, int k1, int lane,
+                                           uint16_t (*xl)[XWIN], float (&acc)[PW][MR], float (&sx)[PW][MR]) {
+    constexpr int NU = ONEG ? 2 : 4;  // 128-k blocks (slots)
+    constexpr int D = depth_bfp4<PW>() < NU ? depth_bfp4<PW>() : NU;
     const int kq = lane >> 4, i = lane & 15;
     const int g0 = k0 >> 8;
     const bool two = !ONEG && k1 - k0 > 256;
-    const int g1 = two ? g0 + 1 : g0;
-    uint32_t xp[NU][MR];
-    uint32_t e[NU / 2][PW];
+    const int nb = two ? NU : 2;
+    int rot[PW];
+#pragma unroll
+    for (int q = 0; q < PW; ++q) rot[q] = ((k0 >> (ONEG ? 8 : 9)) + (NU / 2) * par[q]) & (nb - 1);
+    const XWin<MR> xw = x_win_load<MR>(a, k0, lane);
+    uint32_t e0[PW], e1[PW];  // the chunk's exponent dwords of panel q: group g0's, group g0 + 1's (or g0's again)
+#pragma unroll
+    for (int q = 0; q < PW; ++q) {
+        e0[q] = ld_stream4(eb[q] + (uint32_t)(g0 * 256 + 4 * lane));
+        e1[q] = ld_stream4(eb[q] + (uint32_t)((two ? g0 + 1 : g0) * 256 + 4 * lane));
+    }
     Codes<PW> c[NU];
+    auto issue = [&](int u) {
 #pragma unroll
-    for (int u = 0; u < NU; ++u) {
-        const int b = 2 * (u < 2 ? g0 : g1) + (u & 1);
-        const int kp = b * 128 + kq * 32 + 2 * i;
-        const int kc = min(kp, a.k - 2);  // (K is a multiple of 32: kp < K means kp + 1 < K)
-#pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            const int mc = min(m, a.m - 1);
-            const uint32_t v = *reinterpret_cast<const uint32_t*>(a.x + (size_t)mc * a.ldx + kc);
-            xp[u][m] = v & opaque((kp < a.k && m < a.m) ? 0xFFFFFFFFu : 0u);
+        for (int q = 0; q < PW; ++q) {
+            const int b = real_block(2 * g0 + ((u + rot[q]) & (nb - 1)), a.k);
+            c[u].c[q] = ld_stream16(cb[q] + (uint32_t)(b * 1024 + lane * 16));
         }
-    }
+    };
 #pragma unroll
-    for (int h = 0; h < NU / 2; ++h)
-#pragma unroll
-        for (int q = 0; q < PW; ++q)
-            e[h][q] = ld_stream4(eb[q] + (uint32_t)((h ? g1 : g0) * 256 + 4 * lane));
-#pragma unroll
-    for (int u = 0; u < NU; ++u) {
-        const int b = real_block(2 * (u < 2 ? g0 : g1) + (u & 1), a.k);
-#pragma unroll
-        for (int q = 0; q < PW; ++q) c[u].c[q] = ld_stream16(cb[q] + (uint32_t)(b * 1024 + lane * 16));
-    }
+    for (int u = 0; u < D; ++u) issue(u);
+    x_win_store<MR>(xw, xl, lane);
     // the fold of each panel: every shared exponent of the chunk below 64 (no byte with either of its top two bits set)
     uint32_t mg[PW];
     int eb0[PW];
     bool small[PW];
 #pragma unroll
     for (int q = 0; q < PW; ++q) {
-        const uint32_t any = e[0][q] | e[NU / 2 - 1][q];
-        small[q] = __builtin_amdgcn_ballot_w64((any & 0xC0C0C0C0u) != 0u) == 0ull;
+        small[q] = __builtin_amdgcn_ballot_w64(((e0[q] | e1[q]) & 0xC0C0C0C0u) != 0u) == 0ull;
         mg[q] = small[q] ? BF16_136_2P72 : BF16_136_256;
         eb0[q] = small[q] ? 65 : 129;
     }
 #pragma unroll
     for (int u = 0; u < NU; ++u) {
-        if (u == 2 && !two) break;
-        uint32_t xs[PW][MR];
+        if (u + D < NU) issue(u + D);
+        __builtin_amdgcn_sched_barrier(0);
+        if (ONEG || u < nb) {
+            uint32_t xs[PW][MR];
 #pragma unroll
-        for (int q = 0; q < PW; ++q) {
-            const uint32_t ep = e[u >> 1][q] >> (16 * (u & 1));
+            for (int q = 0; q < PW; ++q) {
+                const int b = (u + rot[q]) & (nb - 1);
+                const uint32_t ep = ((b >> 1) ? e1[q] : e0[q]) >> (16 * (b & 1));
 #pragma unroll
-            for (int m = 0; m < MR; ++m) {
-                const float f0 = __builtin_ldexpf(bf16_to_f32(xp[u][m] & 0xFFFFu), (int)(ep & 0xFFu) - eb0[q]);
-                const float f1 = __builtin_ldexpf(bf16_to_f32(xp[u][m] >> 16), (int)((ep >> 8) & 0xFFu) - eb0[q]);
-                // exact: x has 8 significant bits and a power of two keeps them (a denormal result may lose some;
-                // sx then adds the same truncated values the dot products see)
-                const uint32_t p = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xFFFF0000u);
-                xs[q][m] = p;
-                sx[q][m] += bf16_to_f32(p & 0xFFFFu) + bf16_to_f32(p >> 16);
+                for (int m = 0; m < MR; ++m) {
+                    const uint32_t xp = *reinterpret_cast<const uint32_t*>(&xl[m][128 * b + 32 * kq + 2 * i]);
+                    const float f0 = __builtin_ldexpf(bf16_to_f32(xp & 0xFFFFu), (int)(ep & 0xFFu) - eb0[q]);
+                    const float f1 = __builtin_ldexpf(bf16_to_f32(xp >> 16), (int)((ep >> 8) & 0xFFu) - eb0[q]);
+                    // exact: x has 8 significant bits and a power of two keeps them (a denormal result may lose some;
+                    // sx then adds the same truncated values the dot products see)
+                    const uint32_t pr = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xFFFF0000u);
+                    xs[q][m] = pr;
+                    sx[q][m] += bf16_to_f32(pr & 0xFFFFu) + bf16_to_f32(pr >> 16);
+                }
             }
+            bfp4_step<0, MR, PW>(acc, xs, c[u].c, mg);
         }
-        bfp4_step<0, MR, PW>(acc, xs, c[u].c, mg);
+        __builtin_amdgcn_sched_barrier(0);
     }
     dot_fence(acc);
 #pragma unroll
@@ -524,67 +593,74 @@ __device__ __forceinline__ void chunk_bfp4k(const Args& a, const uint8_t* const*
 // bf16 dot2 of x pairs (as they are) against 136 + q, less 136 times the row's x sum, times the lane's scale. Loads as
 // chunk_bfp4: x first, then the scales, then the codes.
 template <int MR, int PW, bool ONEG = false>
-__device__ __forceinline__ void chunk_int4(const Args& a, const uint8_t* const* cb, const uint16_t* const* gs, int k0,
-                                           int k1, int lane, float (&acc)[PW][MR]) {
-    constexpr int NU = ONEG ? 2 : 4;  // 128-k blocks loaded
+__device__ __forceinline__ void chunk_int4(const Args& a, const uint8_t* const* cb, const uint16_t* const* gs,
+                                           const int (&par)[PW], int k0, int k1, int lane,
+                                           uint16_t (*xl)[XWIN], float (&acc)[PW][MR]) {
+    constexpr int NU = ONEG ? 2 : 4;  // 128-k blocks (slots)
+    constexpr int D = depth_bfp4<PW>() < NU ? depth_bfp4<PW>() : NU;
     const int kq = lane >> 4, i = lane & 15;
     const int g0 = k0 >> 8;
     const bool two = !ONEG && k1 - k0 > 256;
-    const int g1 = two ? g0 + 1 : g0;
-    uint32_t xp[NU][MR];
+    const int nb = two ? NU : 2;
+    int rot[PW];
+#pragma unroll
+    for (int q = 0; q < PW; ++q) rot[q] = ((k0 >> (ONEG ? 8 : 9)) + (NU / 2) * par[q]) & (nb - 1);
+    const XWin<MR> xw = x_win_load<MR>(a, k0, lane);
     uint32_t sc[NU][PW];
+#pragma unroll
+    for (int u = 0; u < NU; ++u)
+#pragma unroll
+        for (int q = 0; q < PW; ++q) {
+            const int b = 2 * g0 + ((u + rot[q]) & (nb - 1));
+            sc[u][q] = __builtin_nontemporal_load(gs[q] + (size_t)b * 64 + lane);
+        }
     Codes<PW> c[NU];
+    auto issue = [&](int u) {
 #pragma unroll
-    for (int u = 0; u < NU; ++u) {
-        const int b = 2 * (u < 2 ? g0 : g1) + (u & 1);
-        const int kp = b * 128 + kq * 32 + 2 * i;
-        const int kc = min(kp, a.k - 2);
-#pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            const int mc = min(m, a.m - 1);
-            const uint32_t v = *reinterpret_cast<const uint32_t*>(a.x + (size_t)mc * a.ldx + kc);
-            xp[u][m] = v & opaque((kp < a.k && m < a.m) ? 0xFFFFFFFFu : 0u);
+        for (int q = 0; q < PW; ++q) {
+            const int b = 2 * g0 + ((u + rot[q]) & (nb - 1));
+            c[u].c[q] = ld_stream16(cb[q] + (uint32_t)(b * 1024 + lane * 16));
         }
-    }
+    };
+#pragma unroll
+    for (int u = 0; u < D; ++u) issue(u);
+    x_win_store<MR>(xw, xl, lane);
 #pragma unroll
     for (int u = 0; u < NU; ++u) {
-        const int b = 2 * (u < 2 ? g0 : g1) + (u & 1);
+        if (u + D < NU) issue(u + D);
+        __builtin_amdgcn_sched_barrier(0);
+        if (ONEG || u < nb) {
+            uint32_t xs[PW][MR];
+            float rs[PW][MR];  // the row's x sum (the 16 lanes' pairs) of panel q's block: 136 times it is in every dot
 #pragma unroll
-        for (int q = 0; q < PW; ++q) sc[u][q] = __builtin_nontemporal_load(gs[q] + (size_t)b * 64 + lane);
-    }
+            for (int q = 0; q < PW; ++q) {
+                const int b = (u + rot[q]) & (nb - 1);
 #pragma unroll
-    for (int u = 0; u < NU; ++u) {
-        const int b = 2 * (u < 2 ? g0 : g1) + (u & 1);
+                for (int m = 0; m < MR; ++m) {
+                    const uint32_t xp = *reinterpret_cast<const uint32_t*>(&xl[m][128 * b + 32 * kq + 2 * i]);
+                    float v = bf16_to_f32(xp & 0xFFFFu) + bf16_to_f32(xp >> 16);
+                    v = wsel::add_xor<8>(wsel::add_xor<4>(wsel::add_xor<2>(wsel::add_xor<1>(v))));  // (over the 16 lanes)
+                    rs[q][m] = 136.f * v;
+                    xs[q][m] = xp;
+                }
+            }
+            float t[PW][MR];
 #pragma unroll
-        for (int q = 0; q < PW; ++q) c[u].c[q] = ld_stream16(cb[q] + (uint32_t)(b * 1024 + lane * 16));
-    }
+            for (int q = 0; q < PW; ++q)
 #pragma unroll
-    for (int u = 0; u < NU; ++u) {
-        if (u == 2 && !two) break;
-        uint32_t xs[PW][MR];
-        float rs[MR];  // the row's x sum (the 16 lanes' pairs): 136 times it is in every dot of the row
+                for (int m = 0; m < MR; ++m) t[q][m] = 0.f;
+            uint32_t mg[PW];
 #pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            float v = bf16_to_f32(xp[u][m] & 0xFFFFu) + bf16_to_f32(xp[u][m] >> 16);
-            v = wsel::add_xor<8>(wsel::add_xor<4>(wsel::add_xor<2>(wsel::add_xor<1>(v))));  // (over the 16 lanes)
-            rs[m] = 136.f * v;
+            for (int q = 0; q < PW; ++q) mg[q] = BF16_136;
+            bfp4_step<0, MR, PW>(t, xs, c[u].c, mg);
+            dot_fence(t);
 #pragma unroll
-            for (int q = 0; q < PW; ++q) xs[q][m] = xp[u][m];
+            for (int q = 0; q < PW; ++q)
+#pragma unroll
+                for (int m = 0; m < MR; ++m)
+                    acc[q][m] = __builtin_fmaf(t[q][m] - rs[q][m], bf16_to_f32(sc[u][q]), acc[q][m]);
         }
-        float t[PW][MR];
-#pragma unroll
-        for (int q = 0; q < PW; ++q)
-#pragma unroll
-            for (int m = 0; m < MR; ++m) t[q][m] = 0.f;
-        uint32_t mg[PW];
-#pragma unroll
-        for (int q = 0; q < PW; ++q) mg[q] = BF16_136;
-        bfp4_step<0, MR, PW>(t, xs, c[u].c, mg);
-        dot_fence(t);
-#pragma unroll
-        for (int q = 0; q < PW; ++q)
-#pragma unroll
-            for (int m = 0; m < MR; ++m) acc[q][m] = __builtin_fmaf(t[q][m] - rs[m], bf16_to_f32(sc[u][q]), acc[q][m]);
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -856,12 +932,13 @@ __device__ __forceinline__ int find_segment(const Args& a, int g) {
     return s;
 }
 
-// the code and exponent bases of the tile's PW panels: plain weights the tile's two panels; interleave_glu weights the
-// gate tile's two panels then the up tile's; gate and up weights apart their tile's two panels each
+// the code and exponent bases of the tile's PW panels, and each panel's parity (of its index in its weight): plain
+// weights the tile's two panels; interleave_glu weights the gate tile's two panels then the up tile's; gate and up
+// weights apart their tile's two panels each
 // GU (the expert gather's gate/up launches, gate and up apart): PW = 2 is a 16-column tile's gate panel and up panel.
 template <int PW, bool GU = false>
 __device__ __forceinline__ void panel_ptrs(const SegDev& sg, int t, int k_pad, const uint8_t* (&cb)[PW],
-                                           const uint8_t* (&eb)[PW]) {
+                                           const uint8_t* (&eb)[PW], int (&par)[PW]) {
 #pragma unroll
     for (int q = 0; q < PW; ++q) {
         int p;
@@ -886,7 +963,14 @@ __device__ __forceinline__ void panel_ptrs(const SegDev& sg, int t, int k_pad, c
         }
         cb[q] = cbase + (size_t)p * sg.pstride;
         eb[q] = ebase + (size_t)p * k_pad;
+        par[q] = p & 1;  // (the panel's parity: its half-turn of the block loaders' slots)
     }
+}
+template <int PW, bool GU = false>
+__device__ __forceinline__ void panel_ptrs(const SegDev& sg, int t, int k_pad, const uint8_t* (&cb)[PW],
+                                           const uint8_t* (&eb)[PW]) {
+    int par[PW];
+    panel_ptrs<PW, GU>(sg, t, k_pad, cb, eb, par);
 }
 
 // ---- the epilogue: the wavefronts' partial sums to the output stages ---------------------------------------------
@@ -1139,7 +1223,9 @@ __device__ __forceinline__ void gemv_body(const Args a) {
     const int fmt = FMT >= 0 ? FMT : sg.fmt;
     const uint8_t* cb[PW];
     const uint8_t* eb[PW];
-    panel_ptrs<PW>(sg, t, a.k_pad, cb, eb);
+    int par[PW];
+    panel_ptrs<PW>(sg, t, a.k_pad, cb, eb, par);
+    __shared__ __align__(16) uint16_t xwin[MAXW][MR][XWIN];  // each wavefront's x window
 
     __shared__ float pre[PRE_FLOATS];
     const EpiPre ep = epi_prefetch<MR, PW>(a, sg, t);
@@ -1158,19 +1244,19 @@ __device__ __forceinline__ void gemv_body(const Args a) {
             for (int m = 0; m < MR; ++m) acc[q][m] = corr[q][m] = 0.f;
         const int k0 = ch * a.kch, k1 = min(k0 + a.kch, a.k_pad);
         if (fmt == DR_BFP8) {
-            chunk_bfp8<MR, PW, ONEG>(a, cb, eb, k0, k1, lane, acc);
+            chunk_bfp8<MR, PW, ONEG>(a, cb, eb, par, k0, k1, lane, xwin[wave], acc);
         } else if (FMT == DR_INT4) {
             const uint16_t* gs[PW];
 #pragma unroll
             for (int q = 0; q < PW; ++q) gs[q] = sg.gscale + (size_t)(PW * t + q) * (a.k_pad / 128) * 64;
-            chunk_int4<MR, PW, ONEG>(a, cb, gs, k0, k1, lane, acc);
+            chunk_int4<MR, PW, ONEG>(a, cb, gs, par, k0, k1, lane, xwin[wave], acc);
         } else if (fmt == DR_BFP4) {
             float sx[PW][MR];
 #pragma unroll
             for (int q = 0; q < PW; ++q)
 #pragma unroll
                 for (int m = 0; m < MR; ++m) sx[q][m] = 0.f;
-            chunk_bfp4<MR, PW, ONEG>(a, cb, eb, k0, k1, lane, acc, sx);
+            chunk_bfp4<MR, PW, ONEG>(a, cb, eb, par, k0, k1, lane, xwin[wave], acc, sx);
             // the wavefront's sum of x' (every lane made distinct x'): its excess is taken off every column
 #pragma unroll
             for (int q = 0; q < PW; ++q)
@@ -1284,7 +1370,9 @@ dr_gemv_moe(const MoeArgs a) {
     }
     const uint8_t* cb[PW];
     const uint8_t* eb[PW];
-    panel_ptrs<PW, moe_n<MOE>()>(sg, t, moe_k<MOE>() ? a.ekp : a.k_pad, cb, eb);
+    int par[PW];
+    panel_ptrs<PW, moe_n<MOE>()>(sg, t, moe_k<MOE>() ? a.ekp : a.k_pad, cb, eb, par);
+    __shared__ __align__(16) uint16_t xwin[moe_k<MOE>() ? MAXW_DOWN : MAXW][MR][XWIN];  // each wavefront's x window
     if constexpr (moe_n<MOE>()) {
 #pragma unroll
         for (int q = 0; q < PW; ++q) {
@@ -1313,7 +1401,7 @@ dr_gemv_moe(const MoeArgs a) {
                 for (int m = 0; m < MR; ++m) wsum[q][m] += wsel::add_xor<32>(wsel::add_xor<16>(acc[q][m]));
             return;
         }
-        chunk_bfp4<MR, PW>(b, cbx, ebx, k0, k1, lane, acc, sx);
+        chunk_bfp4<MR, PW>(b, cbx, ebx, par, k0, k1, lane, xwin[wave], acc, sx);
         // the chunk's column sums less the wavefront's excess, as dr_gemv's
 #pragma unroll
         for (int q = 0; q < PW; ++q)
@@ -2775,8 +2863,9 @@ namespace {
 // the launch's arguments, its panel width, tiles and rows a pass (shared by dr_matmul and dr_workspace_bytes; for the
 // expert gather, gather = true: no 16-column tiles here, and the kblock format allowed)
 int prepare(const dr_launch* L, Args& a, int& pw, int& tiles, int& mr, bool gather = false) {
+    // x rows are read 16 bytes at a time: the rows start 16-byte aligned
     if (L == nullptr || L->x == nullptr || L->y == nullptr || L->m <= 0 || L->k <= 0 || L->k % 32 ||
-        L->ldx < L->k || L->nseg < 1 || L->nseg > 4)
+        L->ldx < L->k || L->ldx % 8 || (reinterpret_cast<uintptr_t>(L->x) & 15) || L->nseg < 1 || L->nseg > 4)
         return DR_EINVAL;
     a.x = reinterpret_cast<const uint16_t*>(L->x);
     a.m = L->m;

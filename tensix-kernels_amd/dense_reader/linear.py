@@ -311,11 +311,14 @@ def choose_blocks(device, x, w, full_sync=False, **forced):
 
 
 def _x2d(x):
-    """x [..., M, K] with leading dims of 1 (or any rank <= 4 that flattens to rows) as a contiguous [M, K] bf16."""
+    """x [..., M, K] with leading dims of 1 (or any rank <= 4 that flattens to rows) as a contiguous [M, K] bf16 whose
+    rows start 16-byte aligned (a copy when x's do not)."""
     assert isinstance(x, torch.Tensor) and x.is_cuda, "dense_reader: x is a bf16 torch tensor on the GPU"
     assert x.dtype == torch.bfloat16, (x.dtype, "dense_reader: x is bf16")
     x2 = x.reshape(-1, x.shape[-1])
-    return x2 if x2.is_contiguous() else x2.contiguous()
+    if not x2.is_contiguous() or x2.data_ptr() % 16:  # (the kernels read x rows 16 bytes at a time)
+        x2 = x2.contiguous() if not x2.is_contiguous() else x2.clone()
+    return x2
 
 
 def _scale_ptr(s, n):

@@ -1141,6 +1141,35 @@ __device__ __forceinline__ void moe_zero(const MoeArgs& a, int t, int unit) {
     }
 }
 
+// The epilogue of a plain launch (one weight, bf16 y, no residual, top-k records or split K): the general epilogue's
+// arithmetic in the same order (so the same bits), without its branches for the other stages. On MI355X the general
+// one's tail cost the north-star launch 0.4 us and the bfloat4_b GLU pair 0.6 (work-stripped copies, one-process A/B).
+template <int ROWS, int PW>
+__device__ __forceinline__ void epilogue_plain(const Args& a, const SegDev& sg, int t, const float* part,
+                                               const float* pre) {
+    constexpr int TW = tile_w<PW>();
+    const int e = threadIdx.x;
+    if (e >= TW * ROWS) return;
+    const int m = e / TW, col = e % TW;
+    const int oc = t * TW + col;
+    if (m >= min(a.m, ROWS) || oc >= sg.n_out) return;
+    const int cq = col >> 4, cc = col & 15;
+    float v;
+    if (PW == 4) {
+        float gsum = 0.f, usum = 0.f;
+        for (int w = 0; w < a.waves; ++w) {
+            gsum += part[((w * PW + cq) * ROWS + m) * 16 + cc];
+            usum += part[((w * PW + 2 + cq) * ROWS + m) * 16 + cc];
+        }
+        v = act_glu(gsum * pre[col], a.act) * (usum * pre[TILE + col]);
+    } else {
+        v = 0.f;
+        for (int w = 0; w < a.waves; ++w) v += part[((w * PW + cq) * ROWS + m) * 16 + cc];
+        v *= pre[col];
+    }
+    reinterpret_cast<uint16_t*>(a.y)[(size_t)m * a.ldy + sg.col0 + oc] = (uint16_t)f32_to_bf16(v);
+}
+
 // ---- split K: the tile's workgroups meet in the workspace ------------------------------------------------------------
 //
 // With splits > 1 each of a tile's workgroups takes cps chunks; it adds its wavefronts' sums (in order), writes them
@@ -1208,13 +1237,14 @@ __device__ __forceinline__ constexpr bool moe_n() {
 // ONEG: the launch's chunks are 256 k, one exponent group each, and the loaders read only that group (the dense
 // kernel keeps its own instantiation: a runtime choice of loader inside it moved the compiler's scheduling of its K
 // loop, NS 12.5 -> 13.1 us)
-template <int MR, int PW, int FMT, bool ONE, bool ONEG>
+template <int MR, int PW, int FMT, bool ONE, bool ONEG, bool PLAIN>
 __device__ __forceinline__ void gemv_body(const Args a) {
     extern __shared__ float part[];  // [W][PW][MR][16]
     __shared__ float tval[MR][TILE];
     __shared__ __align__(16) uint32_t tkey[MR][TILE];
 
-    const int g = blockIdx.x % a.tiles, split = blockIdx.x / a.tiles;
+    // (a plain launch has no split: its workgroup is its tile)
+    const int g = PLAIN ? (int)blockIdx.x : (int)(blockIdx.x % a.tiles), split = PLAIN ? 0 : (int)(blockIdx.x / a.tiles);
     const SegDev& sg = a.seg[find_segment<ONE>(a, g)];
     const int t = g - sg.tile_begin;
     // (the wavefront index is uniform across the wavefront; readfirstlane lets the compiler see it, so the chunk
@@ -1227,8 +1257,12 @@ __device__ __forceinline__ void gemv_body(const Args a) {
     panel_ptrs<PW>(sg, t, a.k_pad, cb, eb, par);
     __shared__ __align__(16) uint16_t xwin[MAXW][MR][XWIN];  // each wavefront's x window
 
+    // the epilogue's scales and residual, read before the K loop so that their latency hides under it; a plain launch
+    // reads its scales after the K loop instead: before it, their dependent scalar and vector loads and branches had
+    // delayed the launch's first weight loads (the north star 11.56 -> 11.28 us, one-process A/B)
     __shared__ float pre[PRE_FLOATS];
-    const EpiPre ep = epi_prefetch<MR, PW>(a, sg, t);
+    EpiPre ep{1.f, 1.f, 0.f};
+    if constexpr (!PLAIN) ep = epi_prefetch<MR, PW>(a, sg, t);
 
     float wsum[PW][MR];  // this wavefront's column sums (lanes 0..15), its chunks added in order
 #pragma unroll
@@ -1284,21 +1318,27 @@ __device__ __forceinline__ void gemv_body(const Args a) {
 #pragma unroll
             for (int m = 0; m < MR; ++m) part[((wave * PW + q) * MR + m) * 16 + lane] = wsum[q][m];
     }
+    if constexpr (PLAIN) ep = epi_prefetch<MR, PW>(a, sg, t);
     epi_stage(ep, pre);
     __syncthreads();
+    if constexpr (PLAIN) {
+        epilogue_plain<MR, PW>(a, sg, t, part, pre);
+        return;
+    }
     const int nparts = gather_splits<MR, PW>(a, g, split, part);
     if (nparts) epilogue<MR, PW>(a, sg, t, part, nparts, tval, tkey, wave, lane, pre);
 }
 
-template <int MR, int PW, int FMT, bool ONE>
+// PLAIN: a plain launch (epilogue_plain), one weight of format FMT
+template <int MR, int PW, int FMT, bool ONE, bool PLAIN = false>
 __global__ __launch_bounds__(512) void dr_gemv(const Args a) {
-    gemv_body<MR, PW, FMT, ONE, false>(a);
+    gemv_body<MR, PW, FMT, ONE, false, PLAIN>(a);
 }
 
 // the same for launches of 256-k chunks (K up to 2048)
-template <int MR, int PW, int FMT, bool ONE>
+template <int MR, int PW, int FMT, bool ONE, bool PLAIN = false>
 __global__ __launch_bounds__(512) void dr_gemv_g1(const Args a) {
-    gemv_body<MR, PW, FMT, ONE, true>(a);
+    gemv_body<MR, PW, FMT, ONE, true, PLAIN>(a);
 }
 
 
@@ -2630,14 +2670,34 @@ void launch_gemv(const Args& a, int grid, hipStream_t st) {
             hipLaunchKernelGGL((dr_gemv<MR, PW, -1, false>), dim3(grid), b, lds, st, a);
         return;
     }
+    // a plain launch (one weight, bf16 y, no residual, top-k records or split K) takes the plain epilogue
+    const bool plain = MR <= 2 && a.rec == nullptr && a.res == nullptr && !a.y_f32 && a.splits == 1;
     switch (a.seg[0].fmt) {
         case DR_BFP8:
+            if constexpr (MR <= 2) {
+                if (plain) {
+                    if (g1)
+                        hipLaunchKernelGGL((dr_gemv_g1<MR, PW, DR_BFP8, true, true>), dim3(grid), b, lds, st, a);
+                    else
+                        hipLaunchKernelGGL((dr_gemv<MR, PW, DR_BFP8, true, true>), dim3(grid), b, lds, st, a);
+                    break;
+                }
+            }
             if (g1)
                 hipLaunchKernelGGL((dr_gemv_g1<MR, PW, DR_BFP8, true>), dim3(grid), b, lds, st, a);
             else
                 hipLaunchKernelGGL((dr_gemv<MR, PW, DR_BFP8, true>), dim3(grid), b, lds, st, a);
             break;
         case DR_BFP4:
+            if constexpr (MR <= 2) {
+                if (plain) {
+                    if (g1)
+                        hipLaunchKernelGGL((dr_gemv_g1<MR, PW, DR_BFP4, true, true>), dim3(grid), b, lds, st, a);
+                    else
+                        hipLaunchKernelGGL((dr_gemv<MR, PW, DR_BFP4, true, true>), dim3(grid), b, lds, st, a);
+                    break;
+                }
+            }
             if (g1)
                 hipLaunchKernelGGL((dr_gemv_g1<MR, PW, DR_BFP4, true>), dim3(grid), b, lds, st, a);
             else
@@ -2645,6 +2705,13 @@ void launch_gemv(const Args& a, int grid, hipStream_t st) {
             break;
         case DR_INT4:
             if constexpr (PW <= 2 && MR <= 2) {
+                if (plain) {
+                    if (g1)
+                        hipLaunchKernelGGL((dr_gemv_g1<MR, PW, DR_INT4, true, true>), dim3(grid), b, lds, st, a);
+                    else
+                        hipLaunchKernelGGL((dr_gemv<MR, PW, DR_INT4, true, true>), dim3(grid), b, lds, st, a);
+                    break;
+                }
                 if (g1)
                     hipLaunchKernelGGL((dr_gemv_g1<MR, PW, DR_INT4, true>), dim3(grid), b, lds, st, a);
                 else

@@ -1182,7 +1182,9 @@ __device__ __forceinline__ void epilogue_plain(const Args& a, const SegDev& sg, 
 // invalidates a whole L2 (it cost 6x the matmul itself). Instead every workspace access is a device-scope atomic
 // (relaxed): such loads and stores go to the device's point of coherence on their own. A workgroup's sums are complete
 // there before it counts itself (each thread waits for its stores, then the barrier), and the last workgroup reads
-// them only after its count has come back. The counters lie at the workspace's start, SPLIT_MAXTILES of them whatever
+// them only after its count has come back. With relaxed accesses that order is the emitted code's, not the memory
+// model's: tests/test_isa_hazards.py checks every kernel's gfx950 code for it (the stores waited for and a barrier
+// before the counter atomic, the loads after its result and a second barrier). The counters lie at the workspace's start, SPLIT_MAXTILES of them whatever
 // the launch's shape, and the sums after them: a workspace shared by launches of any shape never finds an earlier
 // launch's sums where a counter should be zero (a launch of more tiles runs unsplit).
 #ifndef DR_SPLIT_MAXTILES

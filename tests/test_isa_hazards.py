@@ -1,5 +1,5 @@
-"""The gfx950 code of the HIP library, scanned for one hazard the compiler cannot see (CPU only: hipcc emits the device
-assembly here, no GPU runs).
+"""The gfx950 code of the HIP library, scanned for orders the source depends on but cannot state (CPU only: hipcc emits
+the device assembly here, no GPU runs).
 
 The bfloat4_b and int4 loops issue v_dot2c_f32_bf16 (with DPP) from inline asm. A DOT result needs 3 wait states before
 another VALU instruction reads it (a v_dot2c reading it as its own accumulator needs none); the compiler schedules
@@ -71,20 +71,124 @@ def test_scanner_finds_a_planted_hazard():
     assert dot_hazards(head + "\tv_mov_b32_e32 v7, v0\n\tv_add_f32_e32 v5, v3, v4\n")
 
 
-@pytest.mark.skipif(shutil.which("hipcc") is None and not Path("/opt/rocm/bin/hipcc").exists(), reason="no hipcc")
-def test_no_dot_result_read_early(tmp_path):
+@pytest.fixture(scope="module")
+def library_asm(tmp_path_factory):
+    """{source file name: its gfx950 assembly}, compiled once for the module's tests."""
     import __graft_entry__ as G
 
+    if shutil.which("hipcc") is None and not Path(G.HIPCC).exists():
+        pytest.skip("no hipcc")
     hipcc = G.HIPCC if Path(G.HIPCC).exists() else shutil.which("hipcc")
     flags = [f for f in G.FLAGS if f not in ("-shared", "-fPIC")]
-    ndots = 0
+    tmp = tmp_path_factory.mktemp("asm")
+    out = {}
     for src in G.SOURCES:
-        out = tmp_path / (src.stem + ".s")
-        r = subprocess.run([hipcc, *flags, "--cuda-device-only", "-S", str(src), "-o", str(out)], capture_output=True,
+        dst = tmp / (src.stem + ".s")
+        r = subprocess.run([hipcc, *flags, "--cuda-device-only", "-S", str(src), "-o", str(dst)], capture_output=True,
                            text=True)
         assert r.returncode == 0, r.stderr[-2000:]
-        asm = out.read_text()
+        out[src.name] = dst.read_text()
+    return out
+
+
+def test_no_dot_result_read_early(library_asm):
+    ndots = 0
+    for name, asm in library_asm.items():
         ndots += asm.count("v_dot2c_f32_bf16")
         bad = dot_hazards(asm)
-        assert not bad, f"{src.name}: {len(bad)} reads of a dot result inside its wait states, e.g. {bad[:3]}"
+        assert not bad, f"{name}: {len(bad)} reads of a dot result inside its wait states, e.g. {bad[:3]}"
     assert ndots > 0, "no v_dot2c found: the scanner is not looking at the loops it guards"
+
+def _func_bodies(asm):
+    """[(function name, [instruction lines])] of the assembly."""
+    out, name, body = [], None, []
+    for raw in asm.split("\n"):
+        s = raw.strip()
+        m = re.match(r"^(_Z\S+):", s)
+        if m:
+            if name:
+                out.append((name, body))
+            name, body = m.group(1), []
+            continue
+        if name and s and not s.startswith((";", ".")) and not s.endswith(":"):
+            body.append(s)
+    if name:
+        out.append((name, body))
+    return out
+
+
+def meeting_order_faults(asm, names=("dr_gemv", "dr_mfma")):
+    """[(function, what)] for every kernel whose name holds one of `names` and that has the split-K meeting (one
+    returning global_atomic_add, device-scope sc1 stores and loads) where the emitted order breaks the handoff:
+    a partial-sum store not followed by an s_waitcnt vmcnt(0) and an s_barrier before the atomic; or a partial-sum load
+    before the atomic's result is waited for (s_waitcnt vmcnt(0) after it) and a barrier after that."""
+    faults = []
+    for func, body in _func_bodies(asm):
+        if not any(n in func for n in names):
+            continue
+        atomics = [i for i, s in enumerate(body) if s.startswith("global_atomic_add") and re.search(r"\bsc0\b", s)]
+        if not atomics:
+            continue
+        if len(atomics) != 1:
+            faults.append((func, f"{len(atomics)} returning atomics"))
+            continue
+        a = atomics[0]
+        stores = [i for i, s in enumerate(body) if s.startswith("global_store") and re.search(r"\bsc1\b", s)]
+        loads = [i for i, s in enumerate(body) if s.startswith("global_load") and re.search(r"\bsc1\b", s)]
+        before = [i for i in stores if i < a]
+        if not before or not loads:
+            faults.append((func, "no partial-sum stores before the atomic, or no loads"))
+            continue
+        last = max(before)
+        waits = [i for i in range(last + 1, a) if body[i].startswith("s_waitcnt") and "vmcnt(0)" in body[i]]
+        if not waits or not any(body[i] == "s_barrier" for i in range(min(waits) + 1, a)):
+            faults.append((func, "partial-sum stores not waited for (vmcnt(0), then a barrier) before the atomic"))
+        got = [i for i in range(a + 1, len(body)) if body[i].startswith("s_waitcnt") and "vmcnt(0)" in body[i]]
+        bar = [i for i in range(got[0] + 1, len(body)) if body[i] == "s_barrier"] if got else []
+        if not bar or any(i < bar[0] for i in loads):
+            faults.append((func, "a partial-sum load before the atomic's result and the barrier after it"))
+    return faults
+
+
+_MEETING = """_ZN12_GLOBAL__N_17dr_gemvILi1ELi2ELi0ELb1EEEvNS_4ArgsE:
+\tv_add_f32_e32 v7, v7, v8
+\tglobal_store_dword v[8:9], v7, off sc1
+\ts_waitcnt vmcnt(0) expcnt(0) lgkmcnt(0)
+\ts_barrier
+\tglobal_atomic_add v4, v4, v5, s[18:19] sc0
+\ts_waitcnt vmcnt(0)
+\tds_write_b32 v4, v3 offset:6400
+\ts_waitcnt lgkmcnt(0)
+\ts_barrier
+\tglobal_load_dword v7, v[4:5], off sc1
+\tglobal_store_dword v[0:1], v3, off sc1
+"""
+
+
+def test_meeting_scanner_finds_planted_reorders():
+    """The scanner itself: the order above passes; a wait taken out, a store sunk past the atomic or a load hoisted
+    above the barrier (or above the atomic) is flagged."""
+    assert meeting_order_faults(_MEETING) == []
+    no_wait = _MEETING.replace("\ts_waitcnt vmcnt(0) expcnt(0) lgkmcnt(0)\n", "", 1)
+    assert meeting_order_faults(no_wait)
+    sunk = _MEETING.replace("\tglobal_store_dword v[8:9], v7, off sc1\n", "", 1).replace(
+        "\tglobal_atomic_add v4, v4, v5, s[18:19] sc0\n",
+        "\tglobal_atomic_add v4, v4, v5, s[18:19] sc0\n\tglobal_store_dword v[8:9], v7, off sc1\n")
+    assert meeting_order_faults(sunk)
+    hoisted = _MEETING.replace("\tglobal_load_dword v7, v[4:5], off sc1\n", "", 1).replace(
+        "\ts_waitcnt lgkmcnt(0)\n\ts_barrier\n", "\tglobal_load_dword v7, v[4:5], off sc1\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier\n")
+    assert meeting_order_faults(hoisted)
+    early = _MEETING.replace("\tglobal_load_dword v7, v[4:5], off sc1\n", "", 1).replace(
+        "\tglobal_atomic_add", "\tglobal_load_dword v7, v[4:5], off sc1\n\tglobal_atomic_add")
+    assert meeting_order_faults(early)
+
+
+def test_split_k_meeting_order(library_asm):
+    """Every dense kernel with the split-K meeting (dr_gemv, dr_gemv_g1, dr_mfma, the expert gathers) keeps the
+    handoff's order in its gfx950 code."""
+    asm = library_asm["dense_reader.hip"]
+    met = [f for f, body in _func_bodies(asm) if any(n in f for n in ("dr_gemv", "dr_mfma"))
+           and any(s.startswith("global_atomic_add") for s in body)]
+    assert len(met) >= 20, f"only {len(met)} kernels with the meeting found: the scanner is not looking at them"
+    bad = meeting_order_faults(asm)
+    assert not bad, f"{len(bad)} kernels break the split-K handoff's order, e.g. {bad[:3]}"

@@ -159,8 +159,11 @@ int dr_matmul(const dr_launch* launch);
  * nothing but the launch's inputs and outputs. No counterpart in the reference: it is for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). A
  * launch that needs more than DR_SCRATCH_BYTES is refused (DR_ERANGE) before anything is enqueued. Every call on one
- * GPU shares that GPU's array (calls that overlap in time on one GPU race: keep them on one stream); the first call on
- * a device enqueues a fill of its counters on the launch's stream. */
+ * GPU shares that GPU's array (calls that overlap in time on one GPU race: keep them on one stream). The launch's
+ * stream must belong to the current device (else DR_EINVAL). The first call that needs the array on a device clears
+ * its counters with a fill on a stream of the library's own and waits for it before returning, so that call must not
+ * be made under stream capture (refused with DR_EINVAL, nothing enqueued): a caller that captures makes one eager call
+ * first; later calls enqueue only the matmul and can be captured. */
 int dr_matmul_noalloc(const dr_launch* launch);
 int64_t dr_scratch_bytes(void);
 

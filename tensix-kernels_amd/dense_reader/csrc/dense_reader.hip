@@ -3132,20 +3132,59 @@ constexpr int SCRATCH_DEVICES = 64;
 std::mutex scratch_mu;
 void* scratch_addr[SCRATCH_DEVICES];  // (guarded by scratch_mu)
 
-// the current device's scratch address (its counters cleared on first use, on `st`), or null on a HIP error
-void* scratch_for_current_device(hipStream_t st) {
-    int d = 0;
-    if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= SCRATCH_DEVICES) return nullptr;
-    std::lock_guard<std::mutex> lock(scratch_mu);
-    if (scratch_addr[d] == nullptr) {
-        void* ptr = nullptr;
-        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) return nullptr;
-        constexpr int n = (int)(WS_COUNTERS / 4);  // the split-K counters
-        hipLaunchKernelGGL(dr_zero_k, dim3((n + 255) / 256), dim3(256), 0, st, reinterpret_cast<uint32_t*>(ptr), n);
-        if (hipGetLastError() != hipSuccess) return nullptr;
-        scratch_addr[d] = ptr;
+// The scratch of the launch stream's device, or null with `status` set. The stream must belong to the current device
+// (the array's address is looked up with its device current; another device's stream is refused, DR_EINVAL). On a
+// device's first call the counters are cleared by a fill on a stream of the library's own, and the host waits for it
+// before the address is published: a call on any stream then finds them zero. That first call must not be made
+// under stream capture (the fill would be captured, not run): it is refused (DR_EINVAL) and nothing is enqueued, so
+// a caller that captures makes one eager call first.
+void* scratch_for_stream(hipStream_t st, int& status) {
+    int cur = 0;
+    if (hipGetDevice(&cur) != hipSuccess || cur < 0 || cur >= SCRATCH_DEVICES) {
+        status = DR_EHIP;
+        return nullptr;
     }
-    return scratch_addr[d];
+    int sd = cur;
+    if (st != nullptr && hipStreamGetDevice(st, &sd) != hipSuccess) {
+        status = DR_EHIP;
+        return nullptr;
+    }
+    if (sd != cur) {
+        status = DR_EINVAL;
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (scratch_addr[cur] == nullptr) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(st, &cs) != hipSuccess) {
+            status = DR_EHIP;
+            return nullptr;
+        }
+        if (cs != hipStreamCaptureStatusNone) {
+            status = DR_EINVAL;
+            return nullptr;
+        }
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) {
+            status = DR_EHIP;
+            return nullptr;
+        }
+        constexpr int n = (int)(WS_COUNTERS / 4);  // the split-K counters
+        hipStream_t z = nullptr;
+        if (hipStreamCreateWithFlags(&z, hipStreamNonBlocking) != hipSuccess) {
+            status = DR_EHIP;
+            return nullptr;
+        }
+        hipLaunchKernelGGL(dr_zero_k, dim3((n + 255) / 256), dim3(256), 0, z, reinterpret_cast<uint32_t*>(ptr), n);
+        const bool ok = hipGetLastError() == hipSuccess && hipStreamSynchronize(z) == hipSuccess;
+        hipStreamDestroy(z);
+        if (!ok) {
+            status = DR_EHIP;
+            return nullptr;
+        }
+        scratch_addr[cur] = ptr;
+    }
+    return scratch_addr[cur];
 }
 
 
@@ -3198,8 +3237,9 @@ int dr_matmul_noalloc(const dr_launch* L) {
     if (need > DR_SCRATCH_BYTES) return DR_ERANGE;  // (checked before any device call)
     hipStream_t st = S(L->stream);
     if (need > 0) {
-        void* ws = scratch_for_current_device(st);
-        if (ws == nullptr) return DR_EHIP;
+        int status = DR_OK;
+        void* ws = scratch_for_stream(st, status);
+        if (ws == nullptr) return status;
         bind_split(a, ws, pw, mr);
     }
     return run_passes(L, a, tiles, mr, pw, st);

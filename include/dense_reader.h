@@ -200,9 +200,16 @@ typedef struct dr_launch_info {
     int32_t waves;         /* wavefronts a workgroup (each walks its K chunks in turn) */
     int32_t tiles_per_workgroup; /* 2: a 32-row launch of more tiles than CUs, its block-float segments' tiles in
                                     pairs (bf16 segments one a workgroup), else 1 */
-    int32_t reserved[3];
+    int32_t lds_bytes;     /* LDS a workgroup of the first pass's kernel, static and dynamic (0 without a device) */
+    int32_t reserved[2];
 } dr_launch_info;
 int dr_launch_plan(const dr_launch* launch, dr_launch_info* info);
+
+/* Each workgroup of one pass of the launch (info.workgroups of them): five int32 a workgroup, (block, first tile of
+ * the block, tiles, K split, first output column), tiles being 16 or 32 columns (info.tile_cols), the block the
+ * caller's index in seg[]. DR_ERANGE if max_workgroups is smaller. The MI355X counterpart of the `work` list of the
+ * reference's plan (dense_reader/linear.py:355-366: each core's bank, pitch, columns and first output tile). */
+int dr_launch_work(const dr_launch* launch, int32_t* work, int max_workgroups);
 
 /* A plain streaming read of `bytes` (a multiple of 16, 16-byte aligned) at p with every CU: the read ceiling the
  * matmul's weight bandwidth is measured against (bench.py --read-probe). No counterpart in the reference (a

@@ -31,6 +31,7 @@ SYMBOLS = (
     "dr_topk_merge_workspace_bytes",
     "dr_plan",
     "dr_launch_plan",
+    "dr_launch_work",
     "dr_stream_read",
     "dr_status_string",
     "dr_version",
@@ -116,7 +117,8 @@ class LaunchInfo(ctypes.Structure):
         ("tiles_per_record", c_int32),
         ("waves", c_int32),
         ("tiles_per_workgroup", c_int32),
-        ("reserved", c_int32 * 3),
+        ("lds_bytes", c_int32),
+        ("reserved", c_int32 * 2),
     ]
 
 
@@ -209,6 +211,8 @@ def lib():
         L.dr_plan.argtypes = [c_int, c_int, ctypes.POINTER(c_int32), ctypes.POINTER(c_int32), ctypes.POINTER(c_int32)]
         L.dr_launch_plan.restype = c_int
         L.dr_launch_plan.argtypes = [ctypes.POINTER(Launch), ctypes.POINTER(LaunchInfo)]
+        L.dr_launch_work.restype = c_int
+        L.dr_launch_work.argtypes = [ctypes.POINTER(Launch), ctypes.POINTER(c_int32), c_int]
         L.dr_stream_read.restype = c_int
         L.dr_stream_read.argtypes = [c_void_p, c_int64, c_void_p, c_void_p]
         L.dr_status_string.restype = ctypes.c_char_p
@@ -250,6 +254,13 @@ def launch_info(L):
     out = {f: getattr(info, f) for f, _ in LaunchInfo._fields_ if f != "reserved"}
     out["kernel"] = ("gemv", "mfma")[info.kernel]
     return out
+
+
+def launch_work(L, workgroups):
+    """dr_launch_work of a filled dr_launch: [(block, first tile, tiles, split, first output column)] a workgroup."""
+    buf = (c_int32 * (5 * max(1, workgroups)))()
+    check(lib().dr_launch_work(L, buf, workgroups), "dr_launch_work")
+    return [tuple(buf[5 * i : 5 * i + 5]) for i in range(workgroups)]
 
 
 def plan(k, m):

@@ -2654,6 +2654,21 @@ int rows_per_pass(int m) {
     return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
 }
 
+// Set by dr_launch_plan while it walks the launch path: the dense launches then store their kernel's LDS bytes (static
+// plus dynamic) here instead of launching it.
+thread_local size_t* lds_query = nullptr;
+
+template <typename F>
+void fire(F kernel, dim3 grid, dim3 block, size_t lds, hipStream_t st, const Args& a) {
+    if (lds_query != nullptr) {
+        hipFuncAttributes at{};
+        const bool got = hipFuncGetAttributes(&at, reinterpret_cast<const void*>(kernel)) == hipSuccess;
+        *lds_query = lds + (got ? at.sharedSizeBytes : 0);
+        return;
+    }
+    hipLaunchKernelGGL(kernel, grid, block, lds, st, a);
+}
+
 // dynamic LDS of a dense launch: the partial sums, and at 32 rows (the MFMA kernel) the wavefronts' x staging
 size_t dense_lds(const Args& a, int pw, int rows) {
     const size_t part = (size_t)max(a.waves, a.splits) * pw * rows * 16 * sizeof(float);
@@ -2667,9 +2682,9 @@ void launch_gemv(const Args& a, int grid, hipStream_t st) {
     const bool g1 = a.kch == 256;
     if (a.nseg > 1) {
         if (g1)
-            hipLaunchKernelGGL((dr_gemv_g1<MR, PW, -1, false>), dim3(grid), b, lds, st, a);
+            fire((dr_gemv_g1<MR, PW, -1, false>), dim3(grid), b, lds, st, a);
         else
-            hipLaunchKernelGGL((dr_gemv<MR, PW, -1, false>), dim3(grid), b, lds, st, a);
+            fire((dr_gemv<MR, PW, -1, false>), dim3(grid), b, lds, st, a);
         return;
     }
     // a plain launch (one weight, bf16 y, no residual, top-k records or split K) takes the plain epilogue
@@ -2679,49 +2694,49 @@ void launch_gemv(const Args& a, int grid, hipStream_t st) {
             if constexpr (MR <= 2) {
                 if (plain) {
                     if (g1)
-                        hipLaunchKernelGGL((dr_gemv_g1<MR, PW, DR_BFP8, true, true>), dim3(grid), b, lds, st, a);
+                        fire((dr_gemv_g1<MR, PW, DR_BFP8, true, true>), dim3(grid), b, lds, st, a);
                     else
-                        hipLaunchKernelGGL((dr_gemv<MR, PW, DR_BFP8, true, true>), dim3(grid), b, lds, st, a);
+                        fire((dr_gemv<MR, PW, DR_BFP8, true, true>), dim3(grid), b, lds, st, a);
                     break;
                 }
             }
             if (g1)
-                hipLaunchKernelGGL((dr_gemv_g1<MR, PW, DR_BFP8, true>), dim3(grid), b, lds, st, a);
+                fire((dr_gemv_g1<MR, PW, DR_BFP8, true>), dim3(grid), b, lds, st, a);
             else
-                hipLaunchKernelGGL((dr_gemv<MR, PW, DR_BFP8, true>), dim3(grid), b, lds, st, a);
+                fire((dr_gemv<MR, PW, DR_BFP8, true>), dim3(grid), b, lds, st, a);
             break;
         case DR_BFP4:
             if constexpr (MR <= 2) {
                 if (plain) {
                     if (g1)
-                        hipLaunchKernelGGL((dr_gemv_g1<MR, PW, DR_BFP4, true, true>), dim3(grid), b, lds, st, a);
+                        fire((dr_gemv_g1<MR, PW, DR_BFP4, true, true>), dim3(grid), b, lds, st, a);
                     else
-                        hipLaunchKernelGGL((dr_gemv<MR, PW, DR_BFP4, true, true>), dim3(grid), b, lds, st, a);
+                        fire((dr_gemv<MR, PW, DR_BFP4, true, true>), dim3(grid), b, lds, st, a);
                     break;
                 }
             }
             if (g1)
-                hipLaunchKernelGGL((dr_gemv_g1<MR, PW, DR_BFP4, true>), dim3(grid), b, lds, st, a);
+                fire((dr_gemv_g1<MR, PW, DR_BFP4, true>), dim3(grid), b, lds, st, a);
             else
-                hipLaunchKernelGGL((dr_gemv<MR, PW, DR_BFP4, true>), dim3(grid), b, lds, st, a);
+                fire((dr_gemv<MR, PW, DR_BFP4, true>), dim3(grid), b, lds, st, a);
             break;
         case DR_INT4:
             if constexpr (PW <= 2 && MR <= 2) {
                 if (plain) {
                     if (g1)
-                        hipLaunchKernelGGL((dr_gemv_g1<MR, PW, DR_INT4, true, true>), dim3(grid), b, lds, st, a);
+                        fire((dr_gemv_g1<MR, PW, DR_INT4, true, true>), dim3(grid), b, lds, st, a);
                     else
-                        hipLaunchKernelGGL((dr_gemv<MR, PW, DR_INT4, true, true>), dim3(grid), b, lds, st, a);
+                        fire((dr_gemv<MR, PW, DR_INT4, true, true>), dim3(grid), b, lds, st, a);
                     break;
                 }
                 if (g1)
-                    hipLaunchKernelGGL((dr_gemv_g1<MR, PW, DR_INT4, true>), dim3(grid), b, lds, st, a);
+                    fire((dr_gemv_g1<MR, PW, DR_INT4, true>), dim3(grid), b, lds, st, a);
                 else
-                    hipLaunchKernelGGL((dr_gemv<MR, PW, DR_INT4, true>), dim3(grid), b, lds, st, a);
+                    fire((dr_gemv<MR, PW, DR_INT4, true>), dim3(grid), b, lds, st, a);
             }
             break;
         default:  // (bf16 chunks have no exponent groups: one kernel serves every chunk size)
-            hipLaunchKernelGGL((dr_gemv<MR, PW, DR_BF16, true>), dim3(grid), b, lds, st, a);
+            fire((dr_gemv<MR, PW, DR_BF16, true>), dim3(grid), b, lds, st, a);
             break;
     }
 }
@@ -2731,13 +2746,13 @@ void launch_mfma(const Args& a, int grid, hipStream_t st) {
     const dim3 b(64 * a.waves);
     const size_t lds = dense_lds(a, PW, 16 * MT);
     if (a.nseg > 1) {
-        hipLaunchKernelGGL((dr_mfma<MT, PW, -1, false>), dim3(grid), b, lds, st, a);
+        fire((dr_mfma<MT, PW, -1, false>), dim3(grid), b, lds, st, a);
         return;
     }
     switch (a.seg[0].fmt) {
-        case DR_BFP8: hipLaunchKernelGGL((dr_mfma<MT, PW, DR_BFP8, true>), dim3(grid), b, lds, st, a); break;
-        case DR_BFP4: hipLaunchKernelGGL((dr_mfma<MT, PW, DR_BFP4, true>), dim3(grid), b, lds, st, a); break;
-        default: hipLaunchKernelGGL((dr_mfma<MT, PW, DR_BF16, true>), dim3(grid), b, lds, st, a); break;
+        case DR_BFP8: fire((dr_mfma<MT, PW, DR_BFP8, true>), dim3(grid), b, lds, st, a); break;
+        case DR_BFP4: fire((dr_mfma<MT, PW, DR_BFP4, true>), dim3(grid), b, lds, st, a); break;
+        default: fire((dr_mfma<MT, PW, DR_BF16, true>), dim3(grid), b, lds, st, a); break;
     }
 }
 
@@ -2811,13 +2826,13 @@ void launch_pairs(const Args& a, hipStream_t st) {
     const dim3 b(64 * a.waves);
     const size_t lds = max((size_t)a.waves * XS_BYTES, (size_t)2 * a.waves * 2 * 32 * 16 * sizeof(float));
     if (a.nseg > 1) {
-        hipLaunchKernelGGL((dr_mfma_pairs<-1, false>), dim3(a.pairs), b, lds, st, a);
+        fire((dr_mfma_pairs<-1, false>), dim3(a.pairs), b, lds, st, a);
         return;
     }
     switch (a.seg[0].fmt) {
-        case DR_BFP8: hipLaunchKernelGGL((dr_mfma_pairs<DR_BFP8, true>), dim3(a.pairs), b, lds, st, a); break;
-        case DR_BFP4: hipLaunchKernelGGL((dr_mfma_pairs<DR_BFP4, true>), dim3(a.pairs), b, lds, st, a); break;
-        default: hipLaunchKernelGGL((dr_mfma_pairs<DR_BF16, true>), dim3(a.pairs), b, lds, st, a); break;
+        case DR_BFP8: fire((dr_mfma_pairs<DR_BFP8, true>), dim3(a.pairs), b, lds, st, a); break;
+        case DR_BFP4: fire((dr_mfma_pairs<DR_BFP4, true>), dim3(a.pairs), b, lds, st, a); break;
+        default: fire((dr_mfma_pairs<DR_BF16, true>), dim3(a.pairs), b, lds, st, a); break;
     }
 }
 
@@ -3269,6 +3284,54 @@ int dr_launch_plan(const dr_launch* L, dr_launch_info* info) {
     info->records = a.rec != nullptr ? (tiles + a.tk_group - 1) / a.tk_group : 0;
     info->tiles_per_record = a.rec != nullptr ? a.tk_group : 0;
     info->waves = a.waves;
+    // the first pass's kernel, walked without launching: its LDS a workgroup (0 where no device answers)
+    size_t lds = 0;
+    Args p = a;
+    p.m = L->m < mr ? L->m : mr;
+    lds_query = &lds;
+    launch_rows(p, (mr == 32 && p.m <= 16) ? 16 : mr, pw, tiles * a.splits, S(L->stream));
+    lds_query = nullptr;
+    (void)hipGetLastError();
+    info->lds_bytes = (int32_t)lds;
+    return DR_OK;
+}
+
+int dr_launch_work(const dr_launch* L, int32_t* work, int max_workgroups) {
+    Args a{};
+    int pw, tiles, mr;
+    if (work == nullptr || max_workgroups < 0) return DR_EINVAL;
+    if (L != nullptr && L->act == DR_ACT_SWIGLU_OAI) return DR_EINVAL;
+    const int st = prepare(L, a, pw, tiles, mr);
+    if (st != DR_OK) return st;
+    const int wgs = a.pairs > 0 ? a.pairs : tiles * a.splits;
+    if (wgs > max_workgroups) return DR_ERANGE;
+    const int cols = pw == 1 ? 16 : TILE;
+    for (int i = 0; i < wgs; ++i) {
+        // the kernels' own mapping of blockIdx.x (dr_mfma_pairs: pair_begin / pair_tiles; the others: find_segment)
+        int si = 0, t0, nt = 1, split = 0;
+        if (a.pairs > 0) {
+            for (int j = 1; j < a.nseg; ++j)
+                if (i >= a.pair_begin[j]) si = j;
+            t0 = a.pair_tiles[si] * (i - a.pair_begin[si]);
+            nt = min(a.pair_tiles[si], a.seg[si].tiles - t0);
+        } else {
+            const int g = i % tiles;
+            split = i / tiles;
+            for (int j = 1; j < a.nseg; ++j)
+                if (g >= a.seg[j].tile_begin) si = j;
+            t0 = g - a.seg[si].tile_begin;
+        }
+        const SegDev& s = a.seg[si];
+        int block = 0;  // (prepare orders a block list's segments by weight; the caller's index of this one)
+        for (int j = 0; j < L->nseg; ++j)
+            if (L->seg[j].codes == s.codes && L->seg[j].col0 == s.col0) block = j;
+        int32_t* o = work + 5 * (size_t)i;
+        o[0] = block;
+        o[1] = t0;
+        o[2] = nt;
+        o[3] = split;
+        o[4] = s.col0 + t0 * cols;
+    }
     return DR_OK;
 }
 

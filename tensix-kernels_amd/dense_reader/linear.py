@@ -49,6 +49,7 @@ from . import _lib  # noqa: E402
 BFP8_TILE = 1088
 NATIVE_TILES = {bfloat8_b: BFP8_TILE, bfloat4_b: 576, bfloat16: 2048}
 KALIGN = 256  # the packed layout pads K to this
+XCDS = 8  # MI355X's XCDs (each with its own L2): a launch's workgroups go to them in turn
 
 # --- settings (module attributes of the reference, linear.py:52-94) ---------------------------------------------------
 # The Tensix work-split knobs have no meaning on MI355X; they are kept so that code setting them runs, and, as in the
@@ -219,14 +220,54 @@ def held(w, n=None):
     return to_torch(w).reshape(w.k, -1)[:, :n]
 
 
+def _bfp_host(t2, mb):
+    """float32 [R, C] (C a multiple of 16) on the host, rounded to a block float of mb magnitude bits whose exponent is
+    shared by each 16 consecutive values of a row (a face row of the 32 x 32 tile): the conversion the reference's
+    host makes (moe/moe8.py:134-150) and dr_pack makes on the GPU. The shared exponent is the row's largest; each
+    value's 24-bit significand is shifted down by its exponent's distance from it (nothing past 31), rounded to mb
+    bits half to even on the bits shifted out, at most 2^mb - 1; zeros and denormals give 0, and a zero keeps no sign.
+    Returns the values: magnitude * 2^(shared - 127 - (mb - 1)) with the value's sign."""
+    r, c = t2.shape
+    bits = t2.contiguous().view(torch.int32).to(torch.int64).reshape(r, c // 16, 16) & 0xFFFFFFFF
+    exp = (bits >> 23) & 0xFF
+    man = (bits & 0x7FFFFF) | (1 << 23)
+    shared = exp.amax(dim=-1, keepdim=True)
+    diff = shared - exp
+    m = torch.where(diff > 31, torch.zeros_like(man), man >> diff.clamp(max=31))
+    shift = 24 - mb
+    low = m & ((1 << shift) - 1)
+    m = m >> shift
+    half = 1 << (shift - 1)
+    m = m + ((low > half) | ((low == half) & ((m & 1) == 1))).to(torch.int64)
+    m = torch.where(exp == 0, torch.zeros_like(m), m.clamp(max=(1 << mb) - 1))
+    v = torch.ldexp(m.to(torch.float64), (shared - 127 - (mb - 1)).to(torch.float64))
+    v = torch.where(((bits >> 31) == 1) & (m != 0), -v, v)
+    return v.to(torch.float32).reshape(r, c)
+
+
 def block_float(t, dtype, device=None):
-    """t (float [..., rows, cols]) rounded to dtype's grid (face rows along cols), as float32: the values a weight of
-    that dtype holds (reference linear.py:159-163). Runs the packing on the GPU."""
-    d = dev.as_device(device)
+    """t (float [..., rows, cols]) rounded to dtype's grid (the exponent shared along cols, 16 values a face row), as
+    float32 on t's device: the values a weight of that dtype holds (reference linear.py:159-163, a host conversion).
+    Runs on the host (finite inputs); with a device, by packing on that GPU instead (rows a multiple of 32), which
+    gives the same values."""
+    dtype = dev.as_dtype(dtype)
+    assert dtype in NATIVE_TILES, f"dense_reader: weights are bfloat8_b, bfloat4_b or bfloat16, not {dtype}"
     shape = t.shape
-    t2 = t.float().reshape(-1, shape[-1])
-    w = pack(d, t2.T.contiguous(), dtype)  # the matrix [cols, rows] packs as [rows, cols]: face rows along cols
-    return held(w).reshape(shape).to(t.device)
+    t2 = t.detach().float().reshape(-1, shape[-1])
+    if device is not None:
+        d = dev.as_device(device)
+        w = pack(d, t2.T.contiguous(), dtype)  # the matrix [cols, rows] packs as [rows, cols]: face rows along cols
+        return held(w).reshape(shape).to(t.device)
+    h = t2.cpu()
+    if dtype == bfloat16:
+        out = h.to(torch.bfloat16).float()
+    else:
+        c = shape[-1]
+        cp = -(-c // 16) * 16
+        if cp != c:
+            h = torch.nn.functional.pad(h, (0, cp - c))
+        out = _bfp_host(h, 7 if dtype == bfloat8_b else 3)[:, :c]
+    return out.reshape(shape).to(t.device)
 
 
 def reference(x, w, scale=None):
@@ -239,19 +280,98 @@ def reference(x, w, scale=None):
 # --- the plan ---------------------------------------------------------------------------------------------------------
 
 
-def plan(device, x, w, **opts):
-    """The work split of one call: each 32-column output tile is one workgroup of `chunks` wavefronts, each summing a
-    K range of `kch` values; rows go in passes of `rows_per_pass`. It depends on K and the rows only (the reference's
-    plan, linear.py:187-382, is a Tensix core/L1 split; its knobs are accepted by matmul and change nothing)."""
-    k = w.shape[-2]
-    m = x.shape[-2]
-    chunks, kch, rpp = _lib.plan(k, m)
-    return {"K": k, "M": m, "chunks": chunks, "kch": kch, "rows_per_pass": rpp, "KW": kch, "tiles": -(-w.shape[-1] // TILE)}
+def row_slices(x, full_sync=False):
+    """[(first tile row, tile rows)] of x's rows, at most 4 tile rows each (8 with full_sync) (reference linear.py:
+    179-184, where each slice is one program that reads all the weights). matmul needs no slicing: one launch takes
+    all of x's rows, in passes of plan()["rows_per_pass"] inside it. A caller that slices x this way gets each slice's
+    rows from its own matmul (the rows a call takes pick its kernel, so the sums of a slice's rows can differ in their
+    last bits from those of one call over all rows)."""
+    mt = -(-x.shape[-2] // TILE)
+    cap = 8 if full_sync else 4
+    return [(m0, min(cap, mt - m0)) for m0 in range(0, mt, cap)]
+
+
+def plan(
+    device,
+    x,
+    w,
+    cores_per_bank=3,
+    full_sync=False,
+    kb=None,
+    kw=None,
+    sbw=None,
+    split=False,
+    mt=None,
+    rows=False,
+    budget=None,
+    xs=False,
+    noscale=False,
+    glu=False,
+    glu2=False,
+    out32=False,
+    blocks=None,
+    max_banks=None,
+):
+    """The work split of one launch over x's rows (mt tile rows of them, default all), with the reference plan's keys
+    (linear.py:187-382) given their MI355X meaning, and the launch's own (launch_plan's) beside them:
+
+    MT, KT, NT: the tile rows, K tiles and output tiles (32 each). KB: the K tiles of x a workgroup reads (all: x is
+    not cut into blocks). KW: the K tiles of one wavefront's chunk (its unit of work; a workgroup's wavefronts take the
+    chunks in turn). SBW: the 16-column panels one wavefront sums at once (1, 2, or 4 for a GLU's gate and up tiles).
+    NC: the 32-column output tiles a workgroup computes (0.5 for a 16-column tile, 2 for a pair). W_PAGES: the 1 KiB
+    weight blocks of one chunk of one panel (bfloat8_b 64 K, bfloat4_b 128 K, bf16 32 K a block). l1: the LDS bytes a
+    workgroup of the first pass's kernel holds (0 where no device answers). work: [(workgroup, (XCD, block, split,
+    col0, ncols, n0))] for one pass: the XCD whose L2 serves it (workgroups go to the 8 XCDs in turn), the caller's
+    block, the K split it sums, its first column in the block, its columns and its first output column. SEGS: the
+    blocks of a block list (blocks: [(w | (gate, up), col0_tiles[, scale]), ...] as matmul takes it), seg_work: each
+    block's workgroups. sharded: the weight's layout; native: a 32 x 32 tile's bytes in the reference's format.
+    split, rows, xs, noscale, glu, glu2 and the Tensix knobs (cores_per_bank, kb, kw, sbw, budget, max_banks) are
+    kept as given and change nothing; out32 plans an fp32 output. Nothing is launched."""
+    first, target, opts = w, w, {"glu": glu, "out32": out32}
+    if blocks:
+        target = list(blocks)
+        assert is_block_list(target), "dense_reader: blocks is matmul's block list"
+        first, opts = block_entries(target)[0][0], {}
+    L, _, keep = _launch(x, target, None, **opts)
+    info = _lib.launch_info(L)
+    placed = _lib.launch_work(L, info["workgroups"])
+    del keep
+    tc = info["tile_cols"]
+    work = [(i, (i % XCDS, b, sp, t0 * tc, nt * tc, n0)) for i, (b, t0, nt, sp, n0) in enumerate(placed)]
+    segs = L.nseg
+    kblk = {bfloat8_b: 64, bfloat4_b: 128}.get(first.dtype, 32)
+    K, N = first.shape[-2], first.shape[-1]
+    return {
+        "K": K,
+        "M": x.shape[-2],
+        "MT": mt or -(-x.shape[-2] // TILE),
+        "KT": K // TILE,
+        "NT": -(-N // TILE),
+        "KB": K // TILE,
+        "KW": info["kch"] // TILE,
+        "SBW": 4 if glu else tc // 16,
+        "NC": tc * info["tiles_per_workgroup"] / TILE,
+        "W_PAGES": info["kch"] // kblk,
+        "sharded": is_dram_sharded(first),
+        "split": split,
+        "rows": rows,
+        "native": native_tile(first),
+        "xs": xs,
+        "noscale": noscale,
+        "glu": glu,
+        "glu2": glu2,
+        "out32": out32,
+        "SEGS": segs,
+        "seg_work": tuple(tuple(i for i, wk in work if wk[1] == b) for b in range(segs)) if segs > 1 else (),
+        "work": work,
+        "l1": info["lds_bytes"],
+        **info,
+    }
 
 
 def choose(device, x, w, full_sync=False, **forced):
     """[(first tile row, plan)] for x's rows (reference linear.py:455-495): one slice (passes run inside a launch)."""
-    return [(0, plan(device, x, w))]
+    return [(0, plan(device, x, w, **forced))]
 
 
 class BlockListMismatch(ValueError):

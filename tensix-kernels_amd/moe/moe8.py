@@ -127,6 +127,22 @@ def bfp4_values(tiles, kblock=False):
 # --- the reference's Tensix layout helpers (kept: tests and callers read them) ----------------------------------------
 
 
+def _split(total, parts):
+    """[(start, count)]: total in parts as even as they go, the first total % parts parts one larger (reference
+    moe8.py:175-183)."""
+    q, r = divmod(total, parts)
+    starts = [i * q + min(i, r) for i in range(parts)]
+    return [(s0, q + (i < r)) for i, s0 in enumerate(starts)]
+
+
+def gu_pairs(e, bank, banks, pairs=16):
+    """(first pair, pairs) of expert e's gate/up tile pairs that the reference's bank holds: the pairs split over the
+    banks as _split does, the split's parts handed to banks rotated by the expert, so that the larger parts fall on
+    different banks from one expert to the next (reference moe8.py:199-201). Here a layout helper only: the packed
+    experts keep each expert's panels in one place, read by every CU."""
+    return _split(pairs, banks)[(bank - e) % banks]
+
+
 def gu_groups(it, banks):
     """(G, GW): the reference's gate_up column groups per expert and bank, and their width in tiles (reference
     moe8.py:204-212). Here a Tensix dest-size rule only: the layout does not depend on it, but gate_up refuses column

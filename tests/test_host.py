@@ -7,6 +7,7 @@ import re
 import subprocess
 from pathlib import Path
 
+import numpy as np
 import pytest
 import torch
 
@@ -52,10 +53,11 @@ def test_struct_layout_matches_c(tmp_path):
     src = tmp_path / "layout.c"
     src.write_text(
         '#include <stdio.h>\n#include <stddef.h>\n#include "dense_reader.h"\n'
-        "int main(void){printf(\"%zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\\n\", sizeof(dr_segment), sizeof(dr_topk),"
+        "int main(void){printf(\"%zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\\n\", sizeof(dr_segment), sizeof(dr_topk),"
         " sizeof(dr_launch), offsetof(dr_launch, seg), offsetof(dr_launch, topk), offsetof(dr_launch, stream),"
         " offsetof(dr_topk, base), offsetof(dr_segment, col0), offsetof(dr_launch, workspace_bytes),"
-        " sizeof(dr_launch_info), offsetof(dr_launch_info, tiles_per_record), offsetof(dr_launch_info, waves));return 0;}\n"
+        " sizeof(dr_launch_info), offsetof(dr_launch_info, tiles_per_record), offsetof(dr_launch_info, waves),"
+        " offsetof(dr_launch_info, lds_bytes));return 0;}\n"
     )
     exe = tmp_path / "layout"
     subprocess.run(["gcc", "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
@@ -73,6 +75,7 @@ def test_struct_layout_matches_c(tmp_path):
         ctypes.sizeof(_lib.LaunchInfo),
         _lib.LaunchInfo.tiles_per_record.offset,
         _lib.LaunchInfo.waves.offset,
+        _lib.LaunchInfo.lds_bytes.offset,
     ]
     assert got == want
 
@@ -159,6 +162,19 @@ def test_launch_plan_on_the_host():
         assert _lib.lib().dr_launch_plan(ctypes.byref(_ns_launch(**bad)), ctypes.byref(info)) == _lib.DR_EINVAL, bad
     p = _lib.launch_info(_ns_launch(m=100))
     assert (p["rows_per_pass"], p["passes"]) == (32, 4), p
+
+
+def test_launch_work_on_the_host():
+    """dr_launch_work lists the workgroups as the kernels map blockIdx.x: the north star one 32-column tile each, in
+    column order; a split K launch every tile once a split, the splits after each other; 16-column tiles."""
+    L = _ns_launch()
+    work = _lib.launch_work(L, 448)
+    assert work == [(0, i, 1, 0, 32 * i) for i in range(448)]
+    assert _lib.lib().dr_launch_work(ctypes.byref(L), (ctypes.c_int32 * (5 * 447))(), 447) == _lib.DR_ERANGE
+    work = _lib.launch_work(_ns_launch(m=8, k=14336, n=4096), 256)
+    assert work == [(0, i % 128, 1, i // 128, 32 * (i % 128)) for i in range(256)]
+    work = _lib.launch_work(_ns_launch(n=1000), 63)
+    assert work == [(0, i, 1, 0, 16 * i) for i in range(63)]
 
 
 class _FakeWeight:
@@ -290,3 +306,42 @@ def test_pack_cache_files(tmp_path):
     assert pc.cache_read(path, meta, verify=False) is not None
     a = torch.arange(10000, dtype=torch.float32).reshape(100, 100)
     assert pc.fingerprint(a) == pc.fingerprint(a.clone()) and pc.fingerprint(a) != pc.fingerprint(a + 1)
+
+
+def test_row_slices_match_the_reference_rule():
+    """row_slices cuts x's tile rows into slices of 4 (8 with full_sync), the last one short (reference linear.py:
+    179-184): 1 row is one tile row, 200 rows seven, 257 rows nine."""
+    x = torch.zeros(1, 1, 200, 64)
+    assert linear.row_slices(x) == [(0, 4), (4, 3)]
+    assert linear.row_slices(x, full_sync=True) == [(0, 7)]
+    assert linear.row_slices(torch.zeros(1, 64)) == [(0, 1)]
+    assert linear.row_slices(torch.zeros(257, 64), True) == [(0, 8), (8, 1)]
+
+
+@pytest.mark.parametrize("fmt", ["bfp8", "bfp4", "bf16"])
+def test_block_float_on_the_host(fmt):
+    """block_float with no device rounds on the host, bit for bit as the oracle's restatement of the reference's host
+    conversion (and, at a small size, as its Fraction-exact form): ragged columns (a face row cut short is padded with
+    zeros), rows not a multiple of 32, rank 3, values spanning the exponent range (both ends of a row's exponents,
+    zeros, denormals, rounding ties, 2^mb - 1 overflow to the cap)."""
+    from oracle import dense_oracle as O
+
+    g = torch.Generator().manual_seed(5)
+    t = torch.randn(3, 37, 70, generator=g) * torch.exp2(torch.randint(-100, 100, (3, 37, 70), generator=g).float())
+    t[0, 0, :16] = torch.tensor([1.0, -1.0, 2.0**-127, -(2.0**-130), 0.0, -0.0, 1.5, 1.75, 1.875, 1.9375, 1.96875,
+                                 1.984375, 1.9921875, 3.0, 2.0**-30, 2.0**-31])
+    t[1, 5, 32:48] = 2.0**-125 * torch.arange(1, 17).float()
+    t[2, 9, 48:64] = torch.tensor([2.0**127] * 8 + [-(2.0**126)] * 8)
+    dt = {"bfp8": linear.bfloat8_b, "bfp4": linear.bfloat4_b, "bf16": linear.bfloat16}[fmt]
+    got = linear.block_float(t, dt)
+    assert got.shape == t.shape and got.dtype == torch.float32
+    if fmt == "bf16":
+        assert torch.equal(got, t.to(torch.bfloat16).float())
+        return
+    for i in range(3):
+        rows = np.zeros((64, 70), np.float32)  # (the oracle takes whole tiles: the rows round apart)
+        rows[:37] = t[i].numpy()
+        want = O.held(rows, fmt)[:37]
+        assert np.array_equal(got[i].numpy().view(np.uint32), want.astype(np.float32).view(np.uint32)), i
+    small = t[0, :4, :32].numpy()
+    assert np.array_equal(got[0, :4, :32].numpy().astype(np.float64), O.held_exact(small, fmt))

@@ -219,3 +219,18 @@ def test_moe8_route_reference_matches_oracle():
                           **{a: v for a, v in c.items() if a != "bias"})
         assert ids.tolist() == oi, c
         assert np.allclose(w.numpy(), np.array(ow), rtol=1e-12, atol=0), c
+
+
+def test_gu_pairs_rotate_by_expert():
+    """gu_pairs (reference moe8.py:199-201): every bank's parts of an expert's pairs tile them exactly once, in bank
+    order from the part the rotation starts at; the larger parts (16 pairs on 3 banks: 6, 5, 5) move one bank on per
+    expert; 2880 / 32 = 90 pairs on 8 banks give parts of 12 and 11."""
+    assert [moe8.gu_pairs(0, b, 3) for b in range(3)] == [(0, 6), (6, 5), (11, 5)]
+    assert [moe8.gu_pairs(1, b, 3) for b in range(3)] == [(11, 5), (0, 6), (6, 5)]
+    assert [moe8.gu_pairs(2, b, 3) for b in range(3)] == [(6, 5), (11, 5), (0, 6)]
+    for e in range(10):
+        for banks, pairs in ((8, 90), (3, 16), (5, 4), (1, 7)):
+            got = sorted(moe8.gu_pairs(e, b, banks, pairs) for b in range(banks))
+            assert sum(c for _, c in got) == pairs
+            assert all(s0 + c == s1 for (s0, c), (s1, _) in zip(got, got[1:])) and got[0][0] == 0
+            assert {c for _, c in got} <= {pairs // banks, -(-pairs // banks)}

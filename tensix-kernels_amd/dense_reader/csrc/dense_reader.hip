@@ -203,6 +203,15 @@ __device__ __forceinline__ uint32_t opaque(uint32_t v) {
     return v;
 }
 
+// A wave-uniform value made here, in SGPRs: a kernel argument the compiler would otherwise load where it is first
+// used. After the K loop such a load is a scalar-cache miss that waits behind the loop's weight traffic (a block list's
+// segment fields, indexed at run time: three of them in a row held each workgroup of C4's launch ≈ 0.8 us).
+template <typename T>
+__device__ __forceinline__ T pin(T v) {
+    asm volatile("" : "+s"(v));
+    return v;
+}
+
 // the bf16 bits of x[m][k], 0 for a row m or column k outside x (the load is clamped to valid memory, not skipped)
 __device__ __forceinline__ uint32_t x_bits(const Args& a, int m, int k) {
     const int mc = min(m, a.m - 1), kc = min(k, a.k - 1);
@@ -973,6 +982,21 @@ __device__ __forceinline__ void panel_ptrs(const SegDev& sg, int t, int k_pad, c
     panel_ptrs<PW, GU>(sg, t, k_pad, cb, eb, par);
 }
 
+// v + p[0] + p[stride] + ... + p[(n - 1) * stride], added in that order. The LDS reads of 8 terms go out together
+// before any is added: a read a term, each waited for before the next, cost one LDS round trip a term (8 partial sums
+// a column: ≈ 0.4 us at the end of every workgroup).
+__device__ __forceinline__ float sum_parts(float v, const float* p, int n, int stride) {
+    for (int w0 = 0; w0 < n; w0 += 8) {
+        float t[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t[j] = w0 + j < n ? p[(w0 + j) * stride] : 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (w0 + j < n) v += t[j];
+    }
+    return v;
+}
+
 // ---- the epilogue: the wavefronts' partial sums to the output stages ---------------------------------------------
 //
 // part [nparts][PW][ROWS][16]: column sums of panel q, added in order (the wavefronts', or with split K the
@@ -992,11 +1016,8 @@ __device__ __forceinline__ void epilogue(const Args& a, const SegDev& sg, int t,
         float v = 0.f;
         const int cq = col >> 4, cc = col & 15;
         if (PW == 4) {
-            float gsum = 0.f, usum = 0.f;
-            for (int w = 0; w < nparts; ++w) {
-                gsum += part[((w * PW + cq) * ROWS + m) * 16 + cc];
-                usum += part[((w * PW + 2 + cq) * ROWS + m) * 16 + cc];
-            }
+            const float gsum = sum_parts(0.f, part + (cq * ROWS + m) * 16 + cc, nparts, PW * ROWS * 16);
+            const float usum = sum_parts(0.f, part + ((2 + cq) * ROWS + m) * 16 + cc, nparts, PW * ROWS * 16);
             float sgv = 1.f, suv = 1.f;
             if (valid) {
                 if (pre != nullptr) {
@@ -1018,7 +1039,7 @@ __device__ __forceinline__ void epilogue(const Args& a, const SegDev& sg, int t,
             float rv = 0.f;
             if (valid && a.res != nullptr) rv = rpre ? pre[PRE_RES + e] : bf16_to_f32(a.res[(size_t)m * a.ldr + ycol]);
             if (valid && a.res != nullptr && a.res_mode == 2) v = rv;
-            for (int w = 0; w < nparts; ++w) v += part[((w * PW + cq) * ROWS + m) * 16 + cc];
+            v = sum_parts(v, part + (cq * ROWS + m) * 16 + cc, nparts, PW * ROWS * 16);
             if (valid) {
                 v *= pre != nullptr ? pre[col] : load_scale(sg.scale, sg.scale_f32, oc);
                 if (a.res != nullptr && a.res_mode == 1) v += rv;
@@ -1117,11 +1138,8 @@ __device__ __forceinline__ void epilogue_moe(const MoeArgs& a, int t, int unit, 
         const int oc = t * TW + col;  // the column within the expert's
         if (m >= mrows || oc >= a.en) continue;
         const int cq = col >> 4, cc = col & 15;
-        float gsum = 0.f, usum = 0.f;
-        for (int w = 0; w < nparts; ++w) {
-            gsum += part[((w * PW + cq) * ROWS + m) * 16 + cc];
-            usum += part[((w * PW + H + cq) * ROWS + m) * 16 + cc];
-        }
+        float gsum = sum_parts(0.f, part + (cq * ROWS + m) * 16 + cc, nparts, PW * ROWS * 16);
+        float usum = sum_parts(0.f, part + ((H + cq) * ROWS + m) * 16 + cc, nparts, PW * ROWS * 16);
         if (a.bias != nullptr) {
             gsum += bf16_to_f32(a.bias[((size_t)ex * 2 + 0) * a.en + oc]);
             usum += bf16_to_f32(a.bias[((size_t)ex * 2 + 1) * a.en + oc]);
@@ -1156,6 +1174,7 @@ __device__ __forceinline__ void epilogue_plain(const Args& a, const SegDev& sg, 
     const int cq = col >> 4, cc = col & 15;
     float v;
     if (PW == 4) {
+        // (one partial a loop turn: measured faster here than sum_parts' batched reads)
         float gsum = 0.f, usum = 0.f;
         for (int w = 0; w < a.waves; ++w) {
             gsum += part[((w * PW + cq) * ROWS + m) * 16 + cc];
@@ -1206,9 +1225,7 @@ __device__ __forceinline__ int gather_splits(const Args& a, int g, int split, fl
     if (a.splits == 1) return a.waves;
     float* mine = a.wpart + ((size_t)g * a.splits + split) * E;
     for (int e = threadIdx.x; e < E; e += wg_threads(a)) {
-        float v = 0.f;
-        for (int w = 0; w < a.waves; ++w) v += part[w * E + e];
-        st_dev(mine + e, v);
+        st_dev(mine + e, sum_parts(0.f, part + e, a.waves, E));
     }
     __builtin_amdgcn_s_waitcnt(0);  // this thread's stores have reached the point of coherence
     __syncthreads();
@@ -1217,7 +1234,16 @@ __device__ __forceinline__ int gather_splits(const Args& a, int g, int split, fl
     __syncthreads();
     if (!last) return 0;
     const float* all = a.wpart + (size_t)g * a.splits * E;
-    for (int e = threadIdx.x; e < a.splits * E; e += wg_threads(a)) part[e] = ld_dev(all + e);
+    // (4 loads a thread out together: each round trip to the point of coherence is long)
+    const int n = a.splits * E, T = wg_threads(a);
+    for (int e0 = threadIdx.x; e0 < n; e0 += 4 * T) {
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = e0 + j * T < n ? ld_dev(all + e0 + j * T) : 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (e0 + j * T < n) part[e0 + j * T] = v[j];
+    }
     if (threadIdx.x == 0) __hip_atomic_store(a.counters + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     return a.splits;
@@ -1550,6 +1576,8 @@ __device__ __forceinline__ void x_kmask(uint4& v, const Args& a, int k) {
 // x and the columns past the last row's end read as zeros (the rows only reach output rows that are never written;
 // the columns past K are zeroed by x_kmask as in x_row8).
 constexpr int XS_BYTES = 8192;  // a wavefront's staging: 32 rows x 128 k of bf16
+constexpr int PAIR_D = 2;       // dr_mfma_pairs: the steps of codes in flight (bfloat4_b, bf16)
+constexpr int PAIR_RS = 36;     // dr_mfma_pairs: a column's partial sums, 32 rows and 4 of padding
 template <int NCH>
 __device__ __forceinline__ int x_swz(int row) {
     static_assert(NCH == 8 || NCH == 16, "x_swz: 8 or 16 chunks a row");
@@ -1859,18 +1887,55 @@ __device__ __forceinline__ void xl_operands(const Args& a, const uint4* xb, int 
     }
 }
 
+// D: the steps whose codes are in flight (1 or 2; 2 needs an even step count, xl_chunk takes 1 otherwise). x is staged
+// one step ahead in the wavefront's one staging buffer, its loads after the current step's x operands are read out.
+// The issue order, x(s), c(s + D - 1), x(s + 1), c(s + D), ..., keeps the waits exact: the compiler waits for the
+// newest LDS-bound load before any staging read, which then costs nothing the step did not need (its own codes);
+// and every load is issued on every path (the last D steps in a block of their own, issuing no codes), since a load
+// issued under a condition makes the compiler's count assume the worst and wait for every load in flight. The
+// exponent words of a 256-k group load with the group's first step's codes and are read at that step, so one copy of
+// them serves D <= 2.
+template <int D, typename IssueX, typename IssueC, typename Step>
+__device__ __forceinline__ void xl_steps(int ns, IssueX issue_x, IssueC issue_c, Step step) {
+    static_assert(D == 1 || D == 2, "xl_steps: one or two steps of codes in flight");
+    issue_x(0);
+#pragma unroll
+    for (int j = 0; j < D; ++j) issue_c(j, j);
+    int s0 = 0;
+    for (; s0 + D < ns; s0 += D) {
+#pragma unroll
+        for (int j = 0; j < D; ++j)
+            step(s0 + j, j, [&] {
+                issue_x(s0 + j + 1);
+                issue_c(s0 + j + D, j);
+            });
+    }
+#pragma unroll
+    for (int j = 0; j < D; ++j)
+        step(s0 + j, j, [&] {
+            if (j + 1 < D) issue_x(s0 + j + 1);  // (j is a constant here)
+        });
+}
+
 // bfloat8_b: a step is blocks k / 64 and k / 64 + 1 (k0, k1 multiples of 256: a group is two steps); MFMA (b, h) takes
 // k = 64 b + 16 kq + 8 h + j of the step
-template <int PW>
+template <int PW, int D = 1>
 __device__ __forceinline__ void xl_chunk_bfp8(const Args& a, const uint8_t* const* cb, const uint8_t* const* eb, int k0,
                                               int k1, int lane, f32x4 (&acc)[PW][2], uint4* xs) {
+    static_assert(D == 1 || D == 2, "xl_chunk_bfp8: one or two steps in flight");
     const int ns = (k1 - k0) >> 7;
+    if constexpr (D > 1) {
+        if (ns % D) {
+            xl_chunk_bfp8<PW, 1>(a, cb, eb, k0, k1, lane, acc, xs);
+            return;
+        }
+    }
     const XStage<16> xst(a, lane);
-    uint4 cn[2][PW];
+    uint4 cn[D][2][PW];
     uint32_t en[PW], e[PW];
-    auto issue = [&](int s) {
+    auto issue_x = [&](int s) { xst.stage(k0 + 128 * s, xs); };
+    auto issue_c = [&](int s, int slot) {
         const int k = k0 + 128 * s;
-        xst.stage(k, xs);
         if (!(s & 1)) {
 #pragma unroll
             for (int q = 0; q < PW; ++q) en[q] = ld_stream4(eb[q] + (uint32_t)(k + 4 * lane));  // (group k / 256)
@@ -1878,23 +1943,23 @@ __device__ __forceinline__ void xl_chunk_bfp8(const Args& a, const uint8_t* cons
 #pragma unroll
         for (int b = 0; b < 2; ++b)
 #pragma unroll
-            for (int q = 0; q < PW; ++q) cn[b][q] = ld_stream16(cb[q] + (uint32_t)(((k >> 6) + b) * 1024 + lane * 16));
+            for (int q = 0; q < PW; ++q)
+                cn[slot][b][q] = ld_stream16(cb[q] + (uint32_t)(((k >> 6) + b) * 1024 + lane * 16));
     };
-    issue(0);
-    for (int s = 0; s < ns; ++s) {
+    auto step = [&](int s, int j, auto next) {
         const int k = k0 + 128 * s;
         uint4 c[2][PW];
 #pragma unroll
         for (int b = 0; b < 2; ++b)
 #pragma unroll
-            for (int q = 0; q < PW; ++q) c[b][q] = cn[b][q];
+            for (int q = 0; q < PW; ++q) c[b][q] = cn[j][b][q];
         if (!(s & 1)) {
 #pragma unroll
             for (int q = 0; q < PW; ++q) e[q] = en[q];
         }
         uint4 A[4][2];  // [2 b + h][tt]
-        xl_operands<16, 4>(a, xs, k, lane, A, [](int j, int kq) { return 8 * (j >> 1) + 2 * kq + (j & 1); });
-        if (s + 1 < ns) issue(s + 1);
+        xl_operands<16, 4>(a, xs, k, lane, A, [](int jj, int kq) { return 8 * (jj >> 1) + 2 * kq + (jj & 1); });
+        next();
 #pragma unroll
         for (int b = 0; b < 2; ++b)
 #pragma unroll
@@ -1908,49 +1973,110 @@ __device__ __forceinline__ void xl_chunk_bfp8(const Args& a, const uint8_t* cons
                     acc[q][tt] = mfma(A[2 * b + 1][tt], B1, acc[q][tt]);
                 }
             }
+    };
+    xl_steps<D>(ns, issue_x, issue_c, step);
+}
+
+// bfloat8_b one block a step (64 k, its codes 1 KB a panel): half the bytes of a step in flight, for wide tiles
+// (dr_mfma_pairs' four panels); MFMA h of the step takes k = 16 kq + 8 h + j. Sums in the order of xl_chunk_bfp8.
+template <int PW, int D = 1>
+__device__ __forceinline__ void xl_chunk_bfp8_b1(const Args& a, const uint8_t* const* cb, const uint8_t* const* eb,
+                                                 int k0, int k1, int lane, f32x4 (&acc)[PW][2], uint4* xs) {
+    static_assert(D == 1 || D == 2, "xl_chunk_bfp8_b1: one or two steps in flight");
+    const int ns = (k1 - k0) >> 6;
+    if constexpr (D > 1) {
+        if (ns % D) {
+            xl_chunk_bfp8_b1<PW, 1>(a, cb, eb, k0, k1, lane, acc, xs);
+            return;
+        }
     }
+    const XStage<8> xst(a, lane);
+    uint4 cn[D][PW];
+    uint32_t en[PW], e[PW];
+    auto issue_x = [&](int s) { xst.stage(k0 + 64 * s, xs); };
+    auto issue_c = [&](int s, int slot) {
+        const int k = k0 + 64 * s;
+        if (!(s & 3)) {
+#pragma unroll
+            for (int q = 0; q < PW; ++q) en[q] = ld_stream4(eb[q] + (uint32_t)(k + 4 * lane));  // (group k / 256)
+        }
+#pragma unroll
+        for (int q = 0; q < PW; ++q) cn[slot][q] = ld_stream16(cb[q] + (uint32_t)((k >> 6) * 1024 + lane * 16));
+    };
+    auto step = [&](int s, int j, auto next) {
+        const int k = k0 + 64 * s;
+        uint4 c[PW];
+#pragma unroll
+        for (int q = 0; q < PW; ++q) c[q] = cn[j][q];
+        if (!(s & 3)) {
+#pragma unroll
+            for (int q = 0; q < PW; ++q) e[q] = en[q];
+        }
+        uint4 A[2][2];  // [h][tt]
+        xl_operands<8, 2>(a, xs, k, lane, A, [](int jj, int kq) { return 2 * kq + jj; });
+        next();
+#pragma unroll
+        for (int q = 0; q < PW; ++q) {
+            const float sc = __builtin_ldexpf(1.f, (int)((e[q] >> (8 * (s & 3))) & 0xFFu) - 133);
+            const uint4 B0 = b_bfp8<0>(c[q], sc);
+            const uint4 B1 = b_bfp8<1>(c[q], sc);
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                acc[q][tt] = mfma(A[0][tt], B0, acc[q][tt]);
+                acc[q][tt] = mfma(A[1][tt], B1, acc[q][tt]);
+            }
+        }
+    };
+    xl_steps<D>(ns, issue_x, issue_c, step);
 }
 
 // bfloat4_b: a step is block k / 128; MFMA D takes k = 32 kq + 8 D + j of the step
-template <int PW>
+template <int PW, int D = 1>
 __device__ __forceinline__ void xl_chunk_bfp4(const Args& a, const uint8_t* const* cb, const uint8_t* const* eb, int k0,
                                               int k1, int lane, f32x4 (&acc)[PW][2], uint4* xs, uint32_t xbytes = 0) {
+    static_assert(D == 1 || D == 2, "xl_chunk_bfp4: one or two steps in flight");
     const int ns = (k1 - k0) >> 7;
+    if constexpr (D > 1) {
+        if (ns % D) {
+            xl_chunk_bfp4<PW, 1>(a, cb, eb, k0, k1, lane, acc, xs, xbytes);
+            return;
+        }
+    }
     const XStage<16> xst(a, lane, xbytes);
-    uint4 cn[PW];
+    uint4 cn[D][PW];
     uint32_t en[PW], e[PW];
-    auto issue = [&](int s) {
+    auto issue_x = [&](int s) { xst.stage(k0 + 128 * s, xs); };
+    auto issue_c = [&](int s, int slot) {
         const int k = k0 + 128 * s;
-        xst.stage(k, xs);
         if (!(s & 1)) {
 #pragma unroll
             for (int q = 0; q < PW; ++q) en[q] = ld_stream4(eb[q] + (uint32_t)(k + 4 * lane));
         }
 #pragma unroll
-        for (int q = 0; q < PW; ++q) cn[q] = ld_stream16(cb[q] + (uint32_t)(real_block(k >> 7, a.k) * 1024 + lane * 16));
+        for (int q = 0; q < PW; ++q)
+            cn[slot][q] = ld_stream16(cb[q] + (uint32_t)(real_block(k >> 7, a.k) * 1024 + lane * 16));
     };
-    issue(0);
-    for (int s = 0; s < ns; ++s) {
+    auto step = [&](int s, int j, auto next) {
         const int k = k0 + 128 * s;
         uint4 c[PW];
 #pragma unroll
-        for (int q = 0; q < PW; ++q) c[q] = cn[q];
+        for (int q = 0; q < PW; ++q) c[q] = cn[j][q];
         if (!(s & 1)) {
 #pragma unroll
             for (int q = 0; q < PW; ++q) e[q] = en[q];
         }
         uint4 A[4][2];  // [D][tt]
-        xl_operands<16, 4>(a, xs, k, lane, A, [](int j, int kq) { return 4 * kq + j; });
-        if (s + 1 < ns) issue(s + 1);
+        xl_operands<16, 4>(a, xs, k, lane, A, [](int jj, int kq) { return 4 * kq + jj; });
+        next();
 #pragma unroll
         for (int q = 0; q < PW; ++q) {
             const uint32_t ep = e[q] >> (16 * (s & 1));
-            const float s0 = __builtin_ldexpf(1.f, (int)(ep & 0xFFu) - 133);
-            const float s1 = __builtin_ldexpf(1.f, (int)((ep >> 8) & 0xFFu) - 133);
-            const uint4 B0 = b_bfp4<0>(c[q].x, s0, s1);
-            const uint4 B1 = b_bfp4<1>(c[q].y, s0, s1);
-            const uint4 B2 = b_bfp4<2>(c[q].z, s0, s1);
-            const uint4 B3 = b_bfp4<3>(c[q].w, s0, s1);
+            const float s0f = __builtin_ldexpf(1.f, (int)(ep & 0xFFu) - 133);
+            const float s1f = __builtin_ldexpf(1.f, (int)((ep >> 8) & 0xFFu) - 133);
+            const uint4 B0 = b_bfp4<0>(c[q].x, s0f, s1f);
+            const uint4 B1 = b_bfp4<1>(c[q].y, s0f, s1f);
+            const uint4 B2 = b_bfp4<2>(c[q].z, s0f, s1f);
+            const uint4 B3 = b_bfp4<3>(c[q].w, s0f, s1f);
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
                 acc[q][tt] = mfma(A[0][tt], B0, acc[q][tt]);
@@ -1959,43 +2085,52 @@ __device__ __forceinline__ void xl_chunk_bfp4(const Args& a, const uint8_t* cons
                 acc[q][tt] = mfma(A[3][tt], B3, acc[q][tt]);
             }
         }
-    }
+    };
+    xl_steps<D>(ns, issue_x, issue_c, step);
 }
 
 // bf16: a step is 64 k, blocks k / 32 and k / 32 + 1 (its 4 KB of codes a panel pair: half the bfloat8_b step's
 // registers for a 128-k step's 8 KB); MFMA u takes k = 32 u + 8 kq + j of the step
-template <int PW>
+template <int PW, int D = 1>
 __device__ __forceinline__ void xl_chunk_bf16(const Args& a, const uint8_t* const* cb, int k0, int k1, int lane,
                                               f32x4 (&acc)[PW][2], uint4* xs) {
+    static_assert(D == 1 || D == 2, "xl_chunk_bf16: one or two steps in flight");
     const int ns = (k1 - k0) >> 6;
+    if constexpr (D > 1) {
+        if (ns % D) {
+            xl_chunk_bf16<PW, 1>(a, cb, k0, k1, lane, acc, xs);
+            return;
+        }
+    }
     const XStage<8> xst(a, lane);
-    uint4 cn[2][PW];
-    auto issue = [&](int s) {
+    uint4 cn[D][2][PW];
+    auto issue_x = [&](int s) { xst.stage(k0 + 64 * s, xs); };
+    auto issue_c = [&](int s, int slot) {
         const int k = k0 + 64 * s;
-        xst.stage(k, xs);
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
-            for (int q = 0; q < PW; ++q) cn[u][q] = ld_stream16(cb[q] + (uint32_t)(((k >> 5) + u) * 1024 + lane * 16));
+            for (int q = 0; q < PW; ++q)
+                cn[slot][u][q] = ld_stream16(cb[q] + (uint32_t)(((k >> 5) + u) * 1024 + lane * 16));
     };
-    issue(0);
-    for (int s = 0; s < ns; ++s) {
+    auto step = [&](int s, int j, auto next) {
         const int k = k0 + 64 * s;
         uint4 c[2][PW];
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
-            for (int q = 0; q < PW; ++q) c[u][q] = cn[u][q];
+            for (int q = 0; q < PW; ++q) c[u][q] = cn[j][u][q];
         uint4 A[2][2];  // [u][tt]
-        xl_operands<8, 2>(a, xs, k, lane, A, [](int j, int kq) { return 4 * j + kq; });
-        if (s + 1 < ns) issue(s + 1);
+        xl_operands<8, 2>(a, xs, k, lane, A, [](int jj, int kq) { return 4 * jj + kq; });
+        next();
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
             for (int q = 0; q < PW; ++q)
 #pragma unroll
                 for (int tt = 0; tt < 2; ++tt) acc[q][tt] = mfma(A[u][tt], c[u][q], acc[q][tt]);
-    }
+    };
+    xl_steps<D>(ns, issue_x, issue_c, step);
 }
 
 template <int MT, int PW, int FMT, bool ONE>
@@ -2067,7 +2202,7 @@ __global__ __launch_bounds__(512, MT == 2 ? 4 : 1) void dr_mfma(const Args a) { 
 // split K.
 template <int PW, int FMT>  // PW 4: two tiles, 2: one
 __device__ __forceinline__ void pair_tiles(const Args& a, const SegDev& sg, int t0, int nt, int fmt, int wave,
-                                           int lane, float* part, float (*tval)[TILE], uint32_t (*tkey)[TILE]) {
+                                           int lane, float* part) {
     constexpr int ROWS = 32;
     const uint8_t* cb[PW];
     const uint8_t* eb[PW];
@@ -2082,6 +2217,9 @@ __device__ __forceinline__ void pair_tiles(const Args& a, const SegDev& sg, int 
     for (int q = 0; q < PW; ++q)
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) acc[q][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // what the epilogue reads of the arguments, loaded now
+    const int n_out = pin(sg.n_out), col0 = pin(sg.col0), mrows = pin(a.m), ldy = pin(a.ldy), y_f32 = pin(a.y_f32);
+    void* const y = pin(a.y);
     // the tiles' column scales, read before the K loop (after it, their round trip would end the workgroup)
     __shared__ float psc[2][TILE];
     float sc = 1.f;
@@ -2090,31 +2228,61 @@ __device__ __forceinline__ void pair_tiles(const Args& a, const SegDev& sg, int 
     uint4* xs = reinterpret_cast<uint4*>(part) + wave * (XS_BYTES / 16);
     for (int ch = wave; ch < a.chunks; ch += a.waves) {
         const int k0 = ch * a.kch, k1 = min(k0 + a.kch, a.k_pad);
-        if (fmt == DR_BFP8) xl_chunk_bfp8<PW>(a, cb, eb, k0, k1, lane, acc, xs);
-        else if (fmt == DR_BFP4) xl_chunk_bfp4<PW>(a, cb, eb, k0, k1, lane, acc, xs);
-        else xl_chunk_bf16<PW>(a, cb, k0, k1, lane, acc, xs);
+        if (fmt == DR_BFP8) xl_chunk_bfp8_b1<PW, 1>(a, cb, eb, k0, k1, lane, acc, xs);
+        else if (fmt == DR_BFP4) xl_chunk_bfp4<PW, PAIR_D>(a, cb, eb, k0, k1, lane, acc, xs);
+        else xl_chunk_bf16<PW, PAIR_D>(a, cb, k0, k1, lane, acc, xs);
     }
     __syncthreads();  // (every wavefront done with its staging before any partial lands on it)
+    // the partial sums by column: pt[tile][wave][panel][16 columns][PAIR_RS rows] (4 rows of padding: the lanes of a
+    // 16-byte access land on distinct banks), each lane's 4 rows of a 16-row block one 16-byte store
     const int W = a.waves;
 #pragma unroll
     for (int q = 0; q < PW; ++q)
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                part[((((q >> 1) * W + wave) * 2 + (q & 1)) * ROWS + 16 * tt + 4 * (lane >> 4) + j) * 16 + (lane & 15)] =
-                    acc[q][tt][j];
+            *reinterpret_cast<f32x4*>(part + ((((q >> 1) * W + wave) * 2 + (q & 1)) * 16 + (lane & 15)) * PAIR_RS +
+                                      16 * tt + 4 * (lane >> 4)) = acc[q][tt];
     if (su < 2) psc[su][scol] = sc;
     __syncthreads();
-    for (int u = 0; u < PW / 2 && u < nt; ++u)
-        epilogue<ROWS, 2>(a, sg, t0 + u, part + (size_t)u * W * 2 * ROWS * 16, W, tval, tkey, wave, lane, psc[u]);
+    // item (tile u, column c, rows m0 .. m0 + 3), 256 a tile, the workgroup's threads taking them in turn: the
+    // wavefronts' sums in order, times the column's scale, to y
+    for (int it = (int)threadIdx.x; it < 256 * nt; it += 64 * W) {
+        const int u = it >> 8, c = it & 31, m0 = 4 * ((it & 255) >> 5);
+        const int oc = (t0 + u) * TILE + c;
+        if (oc >= n_out || m0 >= mrows) continue;
+        const float* src = part + ((u * W * 2 + (c >> 4)) * 16 + (c & 15)) * PAIR_RS + m0;
+        f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        for (int w0 = 0; w0 < W; w0 += 8) {
+            f32x4 t[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                t[j] = w0 + j < W ? *reinterpret_cast<const f32x4*>(src + (size_t)(w0 + j) * 2 * 16 * PAIR_RS) : v;
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (w0 + j < W) {
+                    v[0] += t[j][0];
+                    v[1] += t[j][1];
+                    v[2] += t[j][2];
+                    v[3] += t[j][3];
+                }
+        }
+        const float scv = psc[u][c];
+        const size_t y0 = (size_t)m0 * ldy + col0 + oc;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (m0 + j >= mrows) break;
+            const float o = v[j] * scv;
+            if (y_f32)
+                reinterpret_cast<float*>(y)[y0 + (size_t)j * ldy] = o;
+            else
+                reinterpret_cast<uint16_t*>(y)[y0 + (size_t)j * ldy] = (uint16_t)f32_to_bf16(o);
+        }
+    }
 }
 
 template <int FMT, bool ONE>
 __global__ __launch_bounds__(512) void dr_mfma_pairs(const Args a) {
-    extern __shared__ float part[];  // x staging during the K loop; then [tiles][W][2][32][16]
-    __shared__ float tval[32][TILE];
-    __shared__ __align__(16) uint32_t tkey[32][TILE];
+    extern __shared__ float part[];  // x staging during the K loop; then [tiles][W][2][16][PAIR_RS]
     const int gp = blockIdx.x;
     int si = 0;
     if (!ONE) {
@@ -2129,9 +2297,9 @@ __global__ __launch_bounds__(512) void dr_mfma_pairs(const Args a) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int fmt = FMT >= 0 ? FMT : sg.fmt;
     if (nt == 2)
-        pair_tiles<4, FMT>(a, sg, t0, nt, fmt, wave, lane, part, tval, tkey);
+        pair_tiles<4, FMT>(a, sg, t0, nt, fmt, wave, lane, part);
     else
-        pair_tiles<2, FMT>(a, sg, t0, nt, fmt, wave, lane, part, tval, tkey);
+        pair_tiles<2, FMT>(a, sg, t0, nt, fmt, wave, lane, part);
 }
 
 template <int MT, int PW, int MOE, bool KB>
@@ -2824,7 +2992,7 @@ hipError_t launch_moe(const MoeArgs& a, int mode, int rows, int pw, int grid, hi
 // one pass of up to `rows` rows
 void launch_pairs(const Args& a, hipStream_t st) {
     const dim3 b(64 * a.waves);
-    const size_t lds = max((size_t)a.waves * XS_BYTES, (size_t)2 * a.waves * 2 * 32 * 16 * sizeof(float));
+    const size_t lds = max((size_t)a.waves * XS_BYTES, (size_t)2 * a.waves * 2 * 16 * PAIR_RS * sizeof(float));
     if (a.nseg > 1) {
         fire((dr_mfma_pairs<-1, false>), dim3(a.pairs), b, lds, st, a);
         return;

@@ -204,8 +204,8 @@ __device__ __forceinline__ uint32_t opaque(uint32_t v) {
 }
 
 // A wave-uniform value made here, in SGPRs: a kernel argument the compiler would otherwise load where it is first
-// used. After the K loop such a load is a scalar-cache miss that waits behind the loop's weight traffic (a block list's
-// segment fields, indexed at run time: three of them in a row held each workgroup of C4's launch ≈ 0.8 us).
+// used (a block list's segment fields, indexed at run time, were three dependent scalar loads at the end of each
+// tile-pair workgroup; loaded before the K loop they wait behind nothing).
 template <typename T>
 __device__ __forceinline__ T pin(T v) {
     asm volatile("" : "+s"(v));
@@ -982,9 +982,9 @@ __device__ __forceinline__ void panel_ptrs(const SegDev& sg, int t, int k_pad, c
     panel_ptrs<PW, GU>(sg, t, k_pad, cb, eb, par);
 }
 
-// v + p[0] + p[stride] + ... + p[(n - 1) * stride], added in that order. The LDS reads of 8 terms go out together
-// before any is added: a read a term, each waited for before the next, cost one LDS round trip a term (8 partial sums
-// a column: ≈ 0.4 us at the end of every workgroup).
+// v + p[0] + p[stride] + ... + p[(n - 1) * stride], added in that order, the LDS reads of 8 terms issued together
+// before any is added (one LDS round trip for 8 terms, where a loop of read-then-add waits for each read in turn).
+// Used by the general and split-K epilogues; the GEMV's plain epilogue keeps its one-term loop, measured faster there.
 __device__ __forceinline__ float sum_parts(float v, const float* p, int n, int stride) {
     for (int w0 = 0; w0 < n; w0 += 8) {
         float t[8];

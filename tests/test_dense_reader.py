@@ -341,13 +341,15 @@ def test_rows_in_passes_bitwise(device, fmt):
         same(f"{fmt} K {k} N {n}: 32 rows against two calls of 16", y32, y16)
 
 
-def test_rows32_tile_pairs(device):
+@pytest.mark.parametrize("k", [768, 800])
+def test_rows32_tile_pairs(device, k):
     """A 32-row launch of more tiles than CUs runs its block-float segments' tiles in pairs, a workgroup each (the
     last of an odd count alone), and its bf16 segments' one a workgroup: a block list of bfloat8_b (129 tiles, odd),
     bf16 (64) and bfloat4_b (65, odd), 258 tiles, equals one call per block bit for bit (each alone has fewer tiles
-    than CUs: no pairs), with scales on the first block and 19 rows (rows past x), and the oracle."""
+    than CUs: no pairs), with scales on the first block and 19 rows (rows past x), and the oracle; K a whole number of
+    the pairs' 64-k steps, and not (800: the last step half past K)."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    k, m = 768, 19
+    m = 19
     spec = [("bfp8", 129), ("bf16", 64), ("bfp4", 65)]
     extra = max(0, cus + 2 - sum(t for _, t in spec))  # (more tiles than this box's CUs)
     spec[1] = ("bf16", spec[1][1] + extra)

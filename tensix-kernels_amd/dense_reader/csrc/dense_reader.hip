@@ -1869,7 +1869,30 @@ __device__ __forceinline__ void mgroup_bf16(const Args& a, const uint8_t* const*
 // flight during the compute of the step before (without that, every wavefront of a workgroup waits for its loads and
 // then computes, together, and the CU idles through half of each). Step s's x operands are read from the staging into
 // registers before step s + 1's loads are issued into the same 8 KB, which keeps a workgroup's LDS small enough for
-// two workgroups a CU. The sums are those of mgroup_* in the same order, so the results are the same bit for bit.
+// two workgroups a CU.
+//
+// A chunk's 128-k units are visited rotated: chunk k0 starts at its unit (k0 / 512) mod 4 and wraps round. The
+// wavefronts of a workgroup take one chunk each, so without the rotation all of them read the same offset of their
+// chunks at once (every chunk starts on an 8 KB boundary of its panel), and those reads pile onto a few of HBM's
+// channels: C4's block list took 16.8 us in the plain order, 15.1 with the rotation, and a plain read of the same
+// bytes in the two orders 14.0 and 11.9 us. Each accumulator still sums its chunk's k in one fixed order, the same in
+// every 32-row kernel of a format (the tile-pair and one-tile kernels, bfloat8_b's 64- and 128-k steps), so their
+// results agree bit for bit. The 16-row kernels (mgroup_*) keep the plain order: rotating theirs measured slower (C3
+// 15.0 -> 15.8 us), so a row's sums there differ in the last bits from the same row's in a 32-row launch. The
+// exponent words of a chunk (one or two 256-k groups) are loaded once, before its first step.
+__device__ __forceinline__ int xl_rot(int k0, int units) { return ((k0 >> 9) & 3) % units; }
+// the chunk's exponent words of panel q: lo for group k0 / 256, hi for the next (the same one again for a one-group
+// chunk, so that no load sits under a branch)
+template <int PW>
+__device__ __forceinline__ void xl_exps(const uint8_t* const* eb, int k0, int k1, int lane, uint32_t (&lo)[PW],
+                                        uint32_t (&hi)[PW]) {
+    const int g0 = k0 >> 8, g1 = k1 - k0 > 256 ? g0 + 1 : g0;
+#pragma unroll
+    for (int q = 0; q < PW; ++q) {
+        lo[q] = ld_stream4(eb[q] + (uint32_t)(g0 * 256 + 4 * lane));
+        hi[q] = ld_stream4(eb[q] + (uint32_t)(g1 * 256 + 4 * lane));
+    }
+}
 
 // x operands of one step of 8 NCH k: A[j][tt] = rows 16 tt + r, the 8 values of chunk chunk(j, kq) (zeroed past K)
 template <int NCH, int NJ, typename F>
@@ -1892,9 +1915,8 @@ __device__ __forceinline__ void xl_operands(const Args& a, const uint4* xb, int 
 // The issue order, x(s), c(s + D - 1), x(s + 1), c(s + D), ..., keeps the waits exact: the compiler waits for the
 // newest LDS-bound load before any staging read, which then costs nothing the step did not need (its own codes);
 // and every load is issued on every path (the last D steps in a block of their own, issuing no codes), since a load
-// issued under a condition makes the compiler's count assume the worst and wait for every load in flight. The
-// exponent words of a 256-k group load with the group's first step's codes and are read at that step, so one copy of
-// them serves D <= 2.
+// issued under a condition makes the compiler's count assume the worst and wait for every load in flight. s counts
+// the steps in the order visited; the chunk functions map it to the rotated step (xl_rot).
 template <int D, typename IssueX, typename IssueC, typename Step>
 __device__ __forceinline__ void xl_steps(int ns, IssueX issue_x, IssueC issue_c, Step step) {
     static_assert(D == 1 || D == 2, "xl_steps: one or two steps of codes in flight");
@@ -1931,15 +1953,14 @@ __device__ __forceinline__ void xl_chunk_bfp8(const Args& a, const uint8_t* cons
         }
     }
     const XStage<16> xst(a, lane);
+    const int rr = xl_rot(k0, ns);
+    auto kof = [&](int s) { const int t = s + rr; return k0 + 128 * (t >= ns ? t - ns : t); };
+    uint32_t elo[PW], ehi[PW];
+    xl_exps<PW>(eb, k0, k1, lane, elo, ehi);
     uint4 cn[D][2][PW];
-    uint32_t en[PW], e[PW];
-    auto issue_x = [&](int s) { xst.stage(k0 + 128 * s, xs); };
+    auto issue_x = [&](int s) { xst.stage(kof(s), xs); };
     auto issue_c = [&](int s, int slot) {
-        const int k = k0 + 128 * s;
-        if (!(s & 1)) {
-#pragma unroll
-            for (int q = 0; q < PW; ++q) en[q] = ld_stream4(eb[q] + (uint32_t)(k + 4 * lane));  // (group k / 256)
-        }
+        const int k = kof(s);
 #pragma unroll
         for (int b = 0; b < 2; ++b)
 #pragma unroll
@@ -1947,16 +1968,13 @@ __device__ __forceinline__ void xl_chunk_bfp8(const Args& a, const uint8_t* cons
                 cn[slot][b][q] = ld_stream16(cb[q] + (uint32_t)(((k >> 6) + b) * 1024 + lane * 16));
     };
     auto step = [&](int s, int j, auto next) {
-        const int k = k0 + 128 * s;
+        const int k = kof(s);
+        const bool hi = k - k0 >= 256;
         uint4 c[2][PW];
 #pragma unroll
         for (int b = 0; b < 2; ++b)
 #pragma unroll
             for (int q = 0; q < PW; ++q) c[b][q] = cn[j][b][q];
-        if (!(s & 1)) {
-#pragma unroll
-            for (int q = 0; q < PW; ++q) e[q] = en[q];
-        }
         uint4 A[4][2];  // [2 b + h][tt]
         xl_operands<16, 4>(a, xs, k, lane, A, [](int jj, int kq) { return 8 * (jj >> 1) + 2 * kq + (jj & 1); });
         next();
@@ -1964,7 +1982,8 @@ __device__ __forceinline__ void xl_chunk_bfp8(const Args& a, const uint8_t* cons
         for (int b = 0; b < 2; ++b)
 #pragma unroll
             for (int q = 0; q < PW; ++q) {
-                const float sc = __builtin_ldexpf(1.f, (int)((e[q] >> (8 * (2 * (s & 1) + b))) & 0xFFu) - 133);
+                const uint32_t ew = hi ? ehi[q] : elo[q];
+                const float sc = __builtin_ldexpf(1.f, (int)((ew >> (8 * (((k >> 6) & 3) + b))) & 0xFFu) - 133);
                 const uint4 B0 = b_bfp8<0>(c[b][q], sc);
                 const uint4 B1 = b_bfp8<1>(c[b][q], sc);
 #pragma unroll
@@ -1991,33 +2010,30 @@ __device__ __forceinline__ void xl_chunk_bfp8_b1(const Args& a, const uint8_t* c
         }
     }
     const XStage<8> xst(a, lane);
+    const int rr = 2 * xl_rot(k0, ns >> 1);  // (in 128-k units, as xl_chunk_bfp8)
+    auto kof = [&](int s) { const int t = s + rr; return k0 + 64 * (t >= ns ? t - ns : t); };
+    uint32_t elo[PW], ehi[PW];
+    xl_exps<PW>(eb, k0, k1, lane, elo, ehi);
     uint4 cn[D][PW];
-    uint32_t en[PW], e[PW];
-    auto issue_x = [&](int s) { xst.stage(k0 + 64 * s, xs); };
+    auto issue_x = [&](int s) { xst.stage(kof(s), xs); };
     auto issue_c = [&](int s, int slot) {
-        const int k = k0 + 64 * s;
-        if (!(s & 3)) {
-#pragma unroll
-            for (int q = 0; q < PW; ++q) en[q] = ld_stream4(eb[q] + (uint32_t)(k + 4 * lane));  // (group k / 256)
-        }
+        const int k = kof(s);
 #pragma unroll
         for (int q = 0; q < PW; ++q) cn[slot][q] = ld_stream16(cb[q] + (uint32_t)((k >> 6) * 1024 + lane * 16));
     };
     auto step = [&](int s, int j, auto next) {
-        const int k = k0 + 64 * s;
+        const int k = kof(s);
+        const bool hi = k - k0 >= 256;
         uint4 c[PW];
 #pragma unroll
         for (int q = 0; q < PW; ++q) c[q] = cn[j][q];
-        if (!(s & 3)) {
-#pragma unroll
-            for (int q = 0; q < PW; ++q) e[q] = en[q];
-        }
         uint4 A[2][2];  // [h][tt]
         xl_operands<8, 2>(a, xs, k, lane, A, [](int jj, int kq) { return 2 * kq + jj; });
         next();
 #pragma unroll
         for (int q = 0; q < PW; ++q) {
-            const float sc = __builtin_ldexpf(1.f, (int)((e[q] >> (8 * (s & 3))) & 0xFFu) - 133);
+            const uint32_t ew = hi ? ehi[q] : elo[q];
+            const float sc = __builtin_ldexpf(1.f, (int)((ew >> (8 * ((k >> 6) & 3))) & 0xFFu) - 133);
             const uint4 B0 = b_bfp8<0>(c[q], sc);
             const uint4 B1 = b_bfp8<1>(c[q], sc);
 #pragma unroll
@@ -2043,34 +2059,30 @@ __device__ __forceinline__ void xl_chunk_bfp4(const Args& a, const uint8_t* cons
         }
     }
     const XStage<16> xst(a, lane, xbytes);
+    const int rr = xl_rot(k0, ns);
+    auto kof = [&](int s) { const int t = s + rr; return k0 + 128 * (t >= ns ? t - ns : t); };
+    uint32_t elo[PW], ehi[PW];
+    xl_exps<PW>(eb, k0, k1, lane, elo, ehi);
     uint4 cn[D][PW];
-    uint32_t en[PW], e[PW];
-    auto issue_x = [&](int s) { xst.stage(k0 + 128 * s, xs); };
+    auto issue_x = [&](int s) { xst.stage(kof(s), xs); };
     auto issue_c = [&](int s, int slot) {
-        const int k = k0 + 128 * s;
-        if (!(s & 1)) {
-#pragma unroll
-            for (int q = 0; q < PW; ++q) en[q] = ld_stream4(eb[q] + (uint32_t)(k + 4 * lane));
-        }
+        const int k = kof(s);
 #pragma unroll
         for (int q = 0; q < PW; ++q)
             cn[slot][q] = ld_stream16(cb[q] + (uint32_t)(real_block(k >> 7, a.k) * 1024 + lane * 16));
     };
     auto step = [&](int s, int j, auto next) {
-        const int k = k0 + 128 * s;
+        const int k = kof(s);
+        const bool hi = k - k0 >= 256;
         uint4 c[PW];
 #pragma unroll
         for (int q = 0; q < PW; ++q) c[q] = cn[j][q];
-        if (!(s & 1)) {
-#pragma unroll
-            for (int q = 0; q < PW; ++q) e[q] = en[q];
-        }
         uint4 A[4][2];  // [D][tt]
         xl_operands<16, 4>(a, xs, k, lane, A, [](int jj, int kq) { return 4 * kq + jj; });
         next();
 #pragma unroll
         for (int q = 0; q < PW; ++q) {
-            const uint32_t ep = e[q] >> (16 * (s & 1));
+            const uint32_t ep = (hi ? ehi[q] : elo[q]) >> (16 * ((k >> 7) & 1));
             const float s0f = __builtin_ldexpf(1.f, (int)(ep & 0xFFu) - 133);
             const float s1f = __builtin_ldexpf(1.f, (int)((ep >> 8) & 0xFFu) - 133);
             const uint4 B0 = b_bfp4<0>(c[q].x, s0f, s1f);
@@ -2103,10 +2115,12 @@ __device__ __forceinline__ void xl_chunk_bf16(const Args& a, const uint8_t* cons
         }
     }
     const XStage<8> xst(a, lane);
+    const int rr = 2 * xl_rot(k0, ns >> 1);  // (in 128-k units)
+    auto kof = [&](int s) { const int t = s + rr; return k0 + 64 * (t >= ns ? t - ns : t); };
     uint4 cn[D][2][PW];
-    auto issue_x = [&](int s) { xst.stage(k0 + 64 * s, xs); };
+    auto issue_x = [&](int s) { xst.stage(kof(s), xs); };
     auto issue_c = [&](int s, int slot) {
-        const int k = k0 + 64 * s;
+        const int k = kof(s);
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
@@ -2114,7 +2128,7 @@ __device__ __forceinline__ void xl_chunk_bf16(const Args& a, const uint8_t* cons
                 cn[slot][u][q] = ld_stream16(cb[q] + (uint32_t)(((k >> 5) + u) * 1024 + lane * 16));
     };
     auto step = [&](int s, int j, auto next) {
-        const int k = k0 + 64 * s;
+        const int k = kof(s);
         uint4 c[2][PW];
 #pragma unroll
         for (int u = 0; u < 2; ++u)
@@ -2780,6 +2794,8 @@ bool narrow_better(int tiles) {
 #ifndef DR_CHUNK_K
 #define DR_CHUNK_K 0
 #endif
+static_assert(DR_CHUNK_K == 0 || (DR_CHUNK_K % 256 == 0 && DR_CHUNK_K <= 512),
+              "a chunk is one or two 256-k exponent groups");
 
 // a workgroup takes at most this many chunks (its MAXW wavefronts two each); more K is split over several workgroups
 // a tile, which then meet in the workspace: fewer splits of more chunks beat more of fewer (K = 14336 at M = 8: 2 x 14

@@ -321,8 +321,10 @@ def test_mfma_narrow_tiles_bitwise(device, fmt):
 @pytest.mark.parametrize("fmt", ["bfp8", "bfp4", "bf16"])
 def test_rows_in_passes_bitwise(device, fmt):
     """Past 32 rows the launch runs passes of 32 (a last pass of at most 16 rows on the 16-row kernel): each pass's rows
-    equal bit for bit those of a call on those rows alone, and the 16- and 32-row kernels sum a row alike. At 300 tiles
-    (the 32-row passes take tile pairs) and at a K split over workgroups."""
+    equal bit for bit those of a call on those rows alone. A row's sums do not depend on the call's other rows within
+    one kernel: 32 rows against calls of 20 (17-32 rows: the 32-row kernel), 16 against calls of 5 (3-16 rows: the
+    16-row kernel). (The two kernels visit a chunk's k in different orders, so across them a row agrees to rounding.)
+    At 300 tiles (the 32-row passes take tile pairs) and at a K split over workgroups."""
     for k, n in ((1024, 9600), (9216, 320)):
         wt = matrix(n, k, 130)
         tw, _ = linear.native_weight(device, wt, DTYPES[fmt])
@@ -337,8 +339,14 @@ def test_rows_in_passes_bitwise(device, fmt):
                 same(f"{fmt} K {k} N {n} rows {m}: rows {r0}-{r1 - 1} against a call on them alone", y[r0:r1], one)
         x, tx = x_input(device, 32, k, 140)
         y32 = host(linear.matmul(tx, tw, None), 32, n)
-        y16 = torch.cat([host(linear.matmul(tx[..., r:r + 16, :].contiguous(), tw, None), 16, n) for r in (0, 16)])
-        same(f"{fmt} K {k} N {n}: 32 rows against two calls of 16", y32, y16)
+        for r0, r1 in ((0, 20), (12, 32)):
+            yr = host(linear.matmul(tx[..., r0:r1, :].contiguous(), tw, None), r1 - r0, n)
+            same(f"{fmt} K {k} N {n}: 32 rows against a call of rows {r0}-{r1 - 1}", y32[r0:r1], yr)
+        y16 = host(linear.matmul(tx[..., :16, :].contiguous(), tw, None), 16, n)
+        check(f"{fmt} K {k} N {n}: 16 rows (the 16-row kernel) against the oracle", y16, ref(x[:16], wk))
+        for r0, r1 in ((0, 5), (11, 16)):
+            yr = host(linear.matmul(tx[..., r0:r1, :].contiguous(), tw, None), r1 - r0, n)
+            same(f"{fmt} K {k} N {n}: 16 rows against a call of rows {r0}-{r1 - 1}", y16[r0:r1], yr)
 
 
 @pytest.mark.parametrize("k", [768, 800])

@@ -1877,9 +1877,11 @@ __device__ __forceinline__ void mgroup_bf16(const Args& a, const uint8_t* const*
 // channels: C4's block list took 16.8 us in the plain order, 15.1 with the rotation, and a plain read of the same
 // bytes in the two orders 14.0 and 11.9 us. Each accumulator still sums its chunk's k in one fixed order, the same in
 // every 32-row kernel of a format (the tile-pair and one-tile kernels, bfloat8_b's 64- and 128-k steps), so their
-// results agree bit for bit. The 16-row kernels (mgroup_*) keep the plain order: rotating theirs measured slower (C3
-// 15.0 -> 15.8 us), so a row's sums there differ in the last bits from the same row's in a 32-row launch. The
-// exponent words of a chunk (one or two 256-k groups) are loaded once, before its first step.
+// results agree bit for bit. bfloat8_b and bf16 are rotated; bfloat4_b keeps the plain order, which measured faster
+// for it (the MoE rows' gate_up 131.8 against 140.5 us). The 16-row kernels (mgroup_*) keep the plain order too:
+// rotating theirs measured slower (C3 15.0 -> 15.8 us), so a row's sums there differ in the last bits from the same
+// row's in a 32-row launch. The rotated kernels load a chunk's exponent words (one or two 256-k groups) once, before
+// its first step.
 __device__ __forceinline__ int xl_rot(int k0, int units) { return ((k0 >> 9) & 3) % units; }
 // the chunk's exponent words of panel q: lo for group k0 / 256, hi for the next (the same one again for a one-group
 // chunk, so that no load sits under a branch)
@@ -1916,7 +1918,9 @@ __device__ __forceinline__ void xl_operands(const Args& a, const uint4* xb, int 
 // newest LDS-bound load before any staging read, which then costs nothing the step did not need (its own codes);
 // and every load is issued on every path (the last D steps in a block of their own, issuing no codes), since a load
 // issued under a condition makes the compiler's count assume the worst and wait for every load in flight. s counts
-// the steps in the order visited; the chunk functions map it to the rotated step (xl_rot).
+// the steps in the order visited; the rotated chunk functions map it to their step (xl_rot). bfloat4_b's, in the
+// plain order, loads a 256-k group's exponent word with the group's first step's codes and reads it at that step, so
+// one copy of it serves D <= 2.
 template <int D, typename IssueX, typename IssueC, typename Step>
 __device__ __forceinline__ void xl_steps(int ns, IssueX issue_x, IssueC issue_c, Step step) {
     static_assert(D == 1 || D == 2, "xl_steps: one or two steps of codes in flight");
@@ -2059,30 +2063,34 @@ __device__ __forceinline__ void xl_chunk_bfp4(const Args& a, const uint8_t* cons
         }
     }
     const XStage<16> xst(a, lane, xbytes);
-    const int rr = xl_rot(k0, ns);
-    auto kof = [&](int s) { const int t = s + rr; return k0 + 128 * (t >= ns ? t - ns : t); };
-    uint32_t elo[PW], ehi[PW];
-    xl_exps<PW>(eb, k0, k1, lane, elo, ehi);
     uint4 cn[D][PW];
-    auto issue_x = [&](int s) { xst.stage(kof(s), xs); };
+    uint32_t en[PW], e[PW];
+    auto issue_x = [&](int s) { xst.stage(k0 + 128 * s, xs); };
     auto issue_c = [&](int s, int slot) {
-        const int k = kof(s);
+        const int k = k0 + 128 * s;
+        if (!(s & 1)) {
+#pragma unroll
+            for (int q = 0; q < PW; ++q) en[q] = ld_stream4(eb[q] + (uint32_t)(k + 4 * lane));
+        }
 #pragma unroll
         for (int q = 0; q < PW; ++q)
             cn[slot][q] = ld_stream16(cb[q] + (uint32_t)(real_block(k >> 7, a.k) * 1024 + lane * 16));
     };
     auto step = [&](int s, int j, auto next) {
-        const int k = kof(s);
-        const bool hi = k - k0 >= 256;
+        const int k = k0 + 128 * s;
         uint4 c[PW];
 #pragma unroll
         for (int q = 0; q < PW; ++q) c[q] = cn[j][q];
+        if (!(s & 1)) {
+#pragma unroll
+            for (int q = 0; q < PW; ++q) e[q] = en[q];
+        }
         uint4 A[4][2];  // [D][tt]
         xl_operands<16, 4>(a, xs, k, lane, A, [](int jj, int kq) { return 4 * kq + jj; });
         next();
 #pragma unroll
         for (int q = 0; q < PW; ++q) {
-            const uint32_t ep = (hi ? ehi[q] : elo[q]) >> (16 * ((k >> 7) & 1));
+            const uint32_t ep = e[q] >> (16 * (s & 1));
             const float s0f = __builtin_ldexpf(1.f, (int)(ep & 0xFFu) - 133);
             const float s1f = __builtin_ldexpf(1.f, (int)((ep >> 8) & 0xFFu) - 133);
             const uint4 B0 = b_bfp4<0>(c[q].x, s0f, s1f);

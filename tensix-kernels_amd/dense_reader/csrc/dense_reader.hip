@@ -1193,9 +1193,9 @@ __device__ __forceinline__ void epilogue_plain(const Args& a, const SegDev& sg, 
 //
 // With splits > 1 each of a tile's workgroups takes cps chunks; it adds its wavefronts' sums (in order), writes them
 // to the workspace and counts itself done; the last one reads every workgroup's sums back, in split order, into part
-// and runs the epilogue (so the sum order is fixed: chunks within a wavefront, wavefronts within a split, splits), then
-// resets the tile's counter for the next launch. Returns the number of partial sums now in part, 0 when this
-// workgroup is not the tile's last.
+// and runs the epilogue (so the sum order is fixed: chunks, or the 16-row kernel's groups, within a wavefront,
+// wavefronts within a split, splits), then resets the tile's counter for the next launch. Returns the number of
+// partial sums now in part, 0 when this workgroup is not the tile's last.
 //
 // The XCDs' L2 caches are not coherent with each other, and an agent-scope release or acquire fence writes back or
 // invalidates a whole L2 (it cost 6x the matmul itself). Instead every workspace access is a device-scope atomic
@@ -2174,7 +2174,7 @@ __global__ __launch_bounds__(512, MT == 2 ? 4 : 1) void dr_mfma(const Args a) { 
     __shared__ float pre[PRE_FLOATS];
     const EpiPre ep = epi_prefetch<ROWS, PW>(a, sg, t);
 
-    f32x4 acc[PW][MT];  // this wavefront's sums over its chunks, in order
+    f32x4 acc[PW][MT];  // this wavefront's sums over its chunks (16 rows: its groups), in order
 #pragma unroll
     for (int q = 0; q < PW; ++q)
 #pragma unroll
@@ -2183,18 +2183,25 @@ __global__ __launch_bounds__(512, MT == 2 ? 4 : 1) void dr_mfma(const Args a) { 
     constexpr bool XL = MT == 2;
     uint4* xs = reinterpret_cast<uint4*>(part) + wave * (XS_BYTES / 16);
     const int ch1 = min((split + 1) * a.cps, a.chunks);
-    for (int ch = split * a.cps + wave; ch < ch1; ch += a.waves) {
-        const int k0 = ch * a.kch, k1 = min(k0 + a.kch, a.k_pad);
-        if constexpr (XL) {
+    if constexpr (XL) {
+        for (int ch = split * a.cps + wave; ch < ch1; ch += a.waves) {
+            const int k0 = ch * a.kch, k1 = min(k0 + a.kch, a.k_pad);
             if (fmt == DR_BFP8) xl_chunk_bfp8<PW>(a, cb, eb, k0, k1, lane, acc, xs);
             else if (fmt == DR_BFP4) xl_chunk_bfp4<PW>(a, cb, eb, k0, k1, lane, acc, xs);
             else xl_chunk_bf16<PW>(a, cb, k0, k1, lane, acc, xs);
-        } else if (fmt == DR_BFP8) {
-            for (int gg = k0 >> 8; gg < (k1 >> 8); ++gg) mgroup_bfp8<MT, PW>(a, cb, eb, gg, lane, acc);
-        } else if (fmt == DR_BFP4) {
-            for (int gg = k0 >> 8; gg < (k1 >> 8); ++gg) mgroup_bfp4<MT, PW>(a, cb, eb, gg, lane, acc);
-        } else {
-            for (int b0 = k0 / 32; b0 < k1 / 32; b0 += 4) mgroup_bf16<MT, PW>(a, cb, b0, lane, acc);
+        }
+    } else {
+        // 16 rows: the wavefronts take the split's 256-k groups in turn (wavefront w groups w, w + W, ...), each one
+        // group at a time, so at any moment they read consecutive 4 KB of a panel rather than the same offset of
+        // their 512-k chunks (C3 15.0 -> 14.5 us; in a plain read of C3's bytes 10.0 -> 9.6)
+        const int g0 = (split * a.cps * a.kch) >> 8, g1 = min(ch1 * a.kch, a.k_pad) >> 8;
+        for (int gg = g0 + wave; gg < g1; gg += a.waves) {
+            if (fmt == DR_BFP8) mgroup_bfp8<MT, PW>(a, cb, eb, gg, lane, acc);
+            else if (fmt == DR_BFP4) mgroup_bfp4<MT, PW>(a, cb, eb, gg, lane, acc);
+            else {
+                mgroup_bf16<MT, PW>(a, cb, 8 * gg, lane, acc);
+                mgroup_bf16<MT, PW>(a, cb, 8 * gg + 4, lane, acc);
+            }
         }
     }
     if constexpr (XL) __syncthreads();  // (every wavefront done with its staging before any partial lands on it)

@@ -349,13 +349,14 @@ def test_rows_in_passes_bitwise(device, fmt):
             same(f"{fmt} K {k} N {n}: 16 rows against a call of rows {r0}-{r1 - 1}", y16[r0:r1], yr)
 
 
-@pytest.mark.parametrize("k", [768, 800])
+@pytest.mark.parametrize("k", [768, 800, 3328])
 def test_rows32_tile_pairs(device, k):
     """A 32-row launch of more tiles than CUs runs its block-float segments' tiles in pairs, a workgroup each (the
     last of an odd count alone), and its bf16 segments' one a workgroup: a block list of bfloat8_b (129 tiles, odd),
     bf16 (64) and bfloat4_b (65, odd), 258 tiles, equals one call per block bit for bit (each alone has fewer tiles
     than CUs: no pairs), with scales on the first block and 19 rows (rows past x), and the oracle; K a whole number of
-    the pairs' 64-k steps, and not (800: the last step half past K)."""
+    the pairs' 64-k steps, and not (800: the last step half past K); 3328: 512-k chunks visited rotated, the last
+    one a single 256-k exponent group."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     m = 19
     spec = [("bfp8", 129), ("bf16", 64), ("bfp4", 65)]

@@ -1871,17 +1871,17 @@ __device__ __forceinline__ void mgroup_bf16(const Args& a, const uint8_t* const*
 // registers before step s + 1's loads are issued into the same 8 KB, which keeps a workgroup's LDS small enough for
 // two workgroups a CU.
 //
-// A chunk's 128-k units are visited rotated: chunk k0 starts at its unit (k0 / 512) mod 4 and wraps round. The
-// wavefronts of a workgroup take one chunk each, so without the rotation all of them read the same offset of their
-// chunks at once (every chunk starts on an 8 KB boundary of its panel), and those reads pile onto a few of HBM's
-// channels: C4's block list took 16.8 us in the plain order, 15.1 with the rotation, and a plain read of the same
-// bytes in the two orders 14.0 and 11.9 us. Each accumulator still sums its chunk's k in one fixed order, the same in
-// every 32-row kernel of a format (the tile-pair and one-tile kernels, bfloat8_b's 64- and 128-k steps), so their
-// results agree bit for bit. bfloat8_b and bf16 are rotated; bfloat4_b keeps the plain order, which measured faster
-// for it (the MoE rows' gate_up 131.8 against 140.5 us). The 16-row kernels (mgroup_*) keep the plain order too:
-// rotating theirs measured slower (C3 15.0 -> 15.8 us), so a row's sums there differ in the last bits from the same
-// row's in a 32-row launch. The rotated kernels load a chunk's exponent words (one or two 256-k groups) once, before
-// its first step.
+// A chunk's 128-k units are visited rotated: chunk k0 starts at its unit (k0 / 512) mod 4 and wraps round (bf16's
+// 64-k steps: at its step (k0 / 512) mod 8). The wavefronts of a workgroup take one chunk each, so without the
+// rotation all of them read the same offset of their chunks at once (every chunk starts on an 8 KB boundary of its
+// panel), and those reads pile onto a few of HBM's channels: C4's block list took 16.8 us in the plain order, 15.1
+// with the rotation, and a plain read of the same bytes in the two orders 14.0 and 11.9 us. Each accumulator still
+// sums its chunk's k in one fixed order, the same in every 32-row kernel of a format (the tile-pair and one-tile
+// kernels, bfloat8_b's 64- and 128-k steps), so their results agree bit for bit. bfloat8_b and bf16 are rotated;
+// bfloat4_b keeps the plain order, which measured faster for it (the MoE rows' gate_up 131.8 against 140.5 us). The
+// 16-row kernel is not rotated either (C3 15.0 -> 15.8 us rotated); its wavefronts take 256-k groups in turn instead
+// (dr_mfma), so a row's sums there differ in the last bits from the same row's in a 32-row launch. The rotated
+// kernels load a chunk's exponent words (one or two 256-k groups) once, before its first step.
 __device__ __forceinline__ int xl_rot(int k0, int units) { return ((k0 >> 9) & 3) % units; }
 // the chunk's exponent words of panel q: lo for group k0 / 256, hi for the next (the same one again for a one-group
 // chunk, so that no load sits under a branch)
@@ -2123,7 +2123,7 @@ __device__ __forceinline__ void xl_chunk_bf16(const Args& a, const uint8_t* cons
         }
     }
     const XStage<8> xst(a, lane);
-    const int rr = 2 * xl_rot(k0, ns >> 1);  // (in 128-k units)
+    const int rr = ((k0 >> 9) & 7) % ns;  // (in its 64-k steps: C4 14.9 -> 14.8 us against 128-k units)
     auto kof = [&](int s) { const int t = s + rr; return k0 + 64 * (t >= ns ? t - ns : t); };
     uint4 cn[D][2][PW];
     auto issue_x = [&](int s) { xst.stage(kof(s), xs); };

@@ -3270,7 +3270,20 @@ int prepare(const dr_launch* L, Args& a, int& pw, int& tiles, int& mr, bool gath
     for (int i = 0; i < a.nseg; ++i) pairable |= a.seg[i].fmt != DR_BF16;
     if (!gather && pairable && mr == 32 && pw == 2 && a.splits == 1 && a.rec == nullptr && a.res == nullptr &&
         tiles > cu_count()) {
+        // here a workgroup's bytes order the segments (a bfloat8_b pair 2 x 1088 B a 32-k step, a bf16 tile 2048, a
+        // bfloat4_b pair 2 x 576; stable), so the heaviest workgroups start first: C4 14.80 -> 14.70 us against the
+        // tiles' order above (its bf16 tiles first)
+        auto wg_bytes = [](int f) { return f == DR_BFP8 ? 2176 : f == DR_BF16 ? 2048 : 1152; };
+        for (int i = 1; i < a.nseg; ++i) {
+            const SegDev v = a.seg[i];
+            int j = i - 1;
+            for (; j >= 0 && wg_bytes(v.fmt) > wg_bytes(a.seg[j].fmt); --j) a.seg[j + 1] = a.seg[j];
+            a.seg[j + 1] = v;
+        }
+        int tb = 0;
         for (int i = 0; i < a.nseg; ++i) {
+            a.seg[i].tile_begin = tb;
+            tb += a.seg[i].tiles;
             a.pair_tiles[i] = a.seg[i].fmt == DR_BF16 ? 1 : 2;
             a.pair_begin[i] = a.pairs;
             a.pairs += (a.seg[i].tiles + a.pair_tiles[i] - 1) / a.pair_tiles[i];

@@ -1,9 +1,9 @@
 """The reference's example and the planner's answers on the GPU.
 
-- The port of the reference's `examples/dense_reader_example.py` that INTEGRATION.md's section 2 gives, run as it is
-  written there (its code block, with the repository's path filled in), then checked as the reference's example
-  checks itself (examples/dense_reader_example.py:24-27): y against the float64 product of x (bf16) and the weight's
-  own held values, relative Frobenius error below 1 %.
+- The port of the reference's `examples/dense_reader_example.py` that the repository's integration guide gives, run
+  as it is written there (the guide's example code block, with the repository's path filled in), then checked as the
+  reference's example checks itself (examples/dense_reader_example.py:24-27): y against the float64 product of x
+  (bf16) and the weight's own held values, relative Frobenius error below 1 %.
 - plan(): the reference plan's keys (dense_reader/linear.py:187-382) for launches of each kernel, its `work` list
   covering every output column once a K split, and its LDS figure the kernel's own.
 - block_float on the host gives the GPU packing's values bit for bit.
